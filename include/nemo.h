@@ -1,0 +1,183 @@
+/*
+ * libnemo: MI355X (gfx950) Nemotron-3-Embed encoder forward pass behind a
+ * plain C ABI. This is the native side of the reference's embedding runtime
+ * (src/webgpu/model.ts NemotronWebGPUModel / NemotronExecutionPlan and the
+ * EmbeddingRuntime / EmbeddingPlan interfaces of
+ * src/webgpu/embedding-engine.ts:7-14). Host bindings (Python ctypes in
+ * nemo_amd, the Node-API addon) call exactly these symbols.
+ *
+ * Conventions: every call returns a nemo_status; on failure
+ * nemo_last_error() returns a message for the calling thread (the reference
+ * throws an Error with that message). No C++ exception crosses the ABI.
+ * Host pointers are copied before a blocking call returns; output buffers
+ * are owned by the caller. Pointers documented as "device" are HIP device
+ * pointers on the context's device.
+ */
+#ifndef NEMO_H
+#define NEMO_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t nemo_status;
+#define NEMO_OK 0
+#define NEMO_ERR_INVALID 1     /* bad argument, shape or format */
+#define NEMO_ERR_MISSING 2     /* a tensor the graph needs was never set */
+#define NEMO_ERR_DEVICE 3      /* HIP runtime failure */
+#define NEMO_ERR_OOM 4         /* device or pinned host allocation failed */
+#define NEMO_ERR_UNSUPPORTED 5 /* valid input this build does not execute */
+
+/* GGML tensor type codes, src/gguf/types.ts:17-23. */
+#define NEMO_TYPE_F32 0
+#define NEMO_TYPE_F16 1
+#define NEMO_TYPE_Q4_0 2
+#define NEMO_TYPE_Q4_K 12
+#define NEMO_TYPE_Q6_K 14
+
+typedef struct nemo_ctx nemo_ctx;
+typedef struct nemo_model nemo_model;
+typedef struct nemo_plan nemo_plan;
+typedef struct nemo_weight nemo_weight;
+
+/* Model shape. The reference hard-codes these (src/webgpu/model.ts:19-28,
+ * src/webgpu/ops.ts:126,186,242,258); here they are parameters so one build
+ * runs both the reference dims and other shapes of the same architecture. */
+typedef struct nemo_dims {
+  int32_t hidden;              /* 2048 */
+  int32_t q_heads;             /* 24 */
+  int32_t kv_heads;            /* 8 */
+  int32_t head_dim;            /* 128 (64 also supported) */
+  int32_t intermediate;        /* 6144 */
+  int32_t layers;              /* 16 */
+  int32_t vocab;               /* 131072 */
+  int32_t merge_after_layer;   /* 4: MERGE_AFTER_LAYER, model.ts:26; 0..layers,
+                                  where == layers merges just before the pool */
+  float rms_epsilon;           /* 1e-5: model.ts:27 */
+  float rope_theta;            /* 1e6: model.ts:28 */
+  int32_t kv_stride_threshold; /* 2048: ops.ts:258 */
+  int32_t kv_stride;           /* 3: ops.ts:258 */
+} nemo_dims;
+
+/* Fills the reference model's constants (src/webgpu/model.ts:19-28). */
+void nemo_dims_reference(nemo_dims* out);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* nemo_last_error(void);
+
+/* Library version string. */
+const char* nemo_version(void);
+
+/* Open a context on HIP device `device` (replaces requestWebGPUDevice,
+ * src/webgpu/device.ts:6-24). */
+nemo_status nemo_init(int32_t device, nemo_ctx** out);
+nemo_status nemo_shutdown(nemo_ctx* ctx);
+
+/* ---- model (src/webgpu/model.ts:236-329) -------------------------------- */
+
+nemo_status nemo_model_create(nemo_ctx* ctx, const nemo_dims* dims, nemo_model** out);
+
+/* Upload one tensor (replaces createBufferWithData per tensor,
+ * src/webgpu/model.ts:264-266,283-286). `dims` are GGUF dims (ne0 first: a
+ * matrix of n rows by k columns is {k, n}). Matrices: NEMO_TYPE_Q4_K or
+ * NEMO_TYPE_Q6_K raw GGUF blocks; norms: NEMO_TYPE_F32; token_embd.weight:
+ * NEMO_TYPE_Q6_K or NEMO_TYPE_F16. Names are the GGUF names; the fused
+ * blk.N.attn_qkv.weight / blk.N.ffn_gate_up.weight may be given directly or
+ * as their parts (attn_q/attn_k/attn_v, ffn_gate/ffn_up), fused at finalize
+ * like combineQ4 (src/webgpu/model.ts:288-304). */
+nemo_status nemo_model_set_tensor(nemo_model* model, const char* name, int32_t ggml_type, const int64_t* dims,
+                                  int32_t n_dims, const void* bytes, size_t n_bytes);
+
+/* Fill every tensor with seeded synthetic weights generated on the device:
+ * matrices N(0, 0.02) quantized to Q4_K (ffn_down to Q6_K), norm weights 1,
+ * token_embd.weight N(0, 0.02) as `embedding_type` (F16 or Q6_K). */
+nemo_status nemo_model_synthesize(nemo_model* model, uint64_t seed, int32_t embedding_type);
+
+/* Validate and fuse; required before nemo_plan_create. Errors name the
+ * missing or malformed tensor (src/webgpu/model.ts:278,291-292,309,315,318). */
+nemo_status nemo_model_finalize(nemo_model* model);
+
+/* Copy a tensor back to the host in its GGUF byte layout. With out == NULL
+ * only *n_bytes is written. */
+nemo_status nemo_model_get_tensor(nemo_model* model, const char* name, int32_t* ggml_type, int64_t* dims4,
+                                  void* out, size_t* n_bytes);
+
+nemo_status nemo_model_destroy(nemo_model* model);
+
+/* ---- execution plan (src/webgpu/model.ts:58-234) ------------------------ */
+
+/* createPlan(batch, sequence) (src/webgpu/model.ts:328): activations for
+ * `batch` requests of up to `sequence` tokens (batch <= 64). */
+nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence, nemo_plan** out);
+
+/* EmbeddingPlan.run (src/webgpu/model.ts:146-176; src/webgpu/embedding-engine.ts:8):
+ * ids[batch * sequence] padded after each request's tokens, lengths[batch]
+ * with 1 <= lengths[b] <= sequence; writes out[batch * hidden] float32,
+ * L2-normalised, in input order. Blocking. n_ids != batch * sequence fails
+ * with 'token buffer does not match execution plan' (model.ts:147). */
+nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, const uint32_t* lengths,
+                          size_t n_lengths, float* out);
+
+/* Same graph with ids and out as device pointers, enqueued on `stream`
+ * (hipStream_t; NULL = the plan's own stream); lengths are host values.
+ * Returns once enqueued. */
+nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const uint32_t* lengths, size_t n_lengths,
+                                 float* d_out, void* stream);
+
+/* profile() (src/webgpu/model.ts:178-224): milliseconds per stage, summed
+ * over layers, in the order of nemo_profile_stage_name. */
+nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids, const uint32_t* lengths,
+                              size_t n_lengths, float* stage_ms, int32_t n_stages);
+int32_t nemo_profile_stage_count(void);
+const char* nemo_profile_stage_name(int32_t index);
+
+/* destroy() (src/webgpu/model.ts:141-144). */
+nemo_status nemo_plan_destroy(nemo_plan* plan);
+
+/* Copy one activation buffer of the last run to the host, for stage-wise
+ * parity checks (the reference's buffers of src/webgpu/model.ts:80-94 are
+ * debuggable the same way through readF16Buffer, src/main.ts:24-34). Names:
+ * "x_full", "norm_full", "x_merged", "norm_merged", "qkv", "q", "k",
+ * "attention", "delta", "gate_up", "ffn" (f16, packed rows of the last layer
+ * that wrote them) and "embeddings" (float). With out == NULL only *n_bytes is
+ * written (the buffer's capacity). Blocks until the plan's work is done. */
+nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, size_t* n_bytes);
+
+/* ---- kernel level (src/webgpu/quant-matmul.ts:438-563) ------------------- */
+
+/* Upload one quantized matrix of n rows by k columns (k % 256 == 0) from raw
+ * GGUF bytes: QuantMatmulKernel.createRun's weight buffer
+ * (src/webgpu/quant-matmul.ts:503-509). Types Q4_K and Q6_K. */
+nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int32_t k, const void* bytes,
+                               size_t n_bytes, nemo_weight** out);
+nemo_status nemo_weight_destroy(nemo_weight* weight);
+
+#define NEMO_MATMUL_AUTO 0 /* GEMV for m <= 16, else the MFMA GEMM */
+#define NEMO_MATMUL_GEMM 1
+#define NEMO_MATMUL_GEMV 2
+
+/* Y[m, n] = f16(X[m, k] W[n, k]^T), fp32 accumulate; d_x f16 [m, k] and d_y
+ * f16 [m, n] are device pointers (createRun + dispatch,
+ * src/webgpu/quant-matmul.ts:503-563). */
+nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y, int32_t algo,
+                               void* stream);
+
+/* Decode the uploaded matrix to float32 [n, k] (device pointer); bit-exact
+ * with dequantizeQ4KBlock / dequantizeQ6KBlock (src/gguf/quantization.ts:19-74). */
+nemo_status nemo_weight_dequantize(nemo_weight* weight, float* d_out, void* stream);
+
+/* Decode raw GGUF blocks at a 16-byte aligned device pointer to float32
+ * and/or f16 (either output may be NULL): dequantizeQ4KBlock,
+ * dequantizeQ6KBlock, dequantizeQ40Block (src/gguf/quantization.ts:19-74).
+ * n_values must be a whole number of blocks. */
+nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_values, float* d_out_f32,
+                            uint16_t* d_out_f16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEMO_H */

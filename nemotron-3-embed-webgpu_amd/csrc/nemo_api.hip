@@ -1,0 +1,869 @@
+// C ABI of libnemo: context, model (weights), execution plan (activations and
+// the 16-layer graph) and kernel-level entry points. Mirrors
+// src/webgpu/model.ts (NemotronWebGPUModel, NemotronExecutionPlan) and
+// src/webgpu/quant-matmul.ts (QuantMatmulKernel).
+#include <math.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/nemo.h"
+#include "nemo_common.h"
+#include "nemo_ops.h"
+#include "nemo_quant.h"
+#include "nemo_synth.h"
+
+using namespace nemo;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct NemoError : std::runtime_error {
+  nemo_status status;
+  NemoError(nemo_status s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+
+[[noreturn]] void fail(nemo_status s, const std::string& m) { throw NemoError(s, m); }
+
+void hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  if (e == hipErrorOutOfMemory) fail(NEMO_ERR_OOM, std::string(what) + ": out of device memory");
+  fail(NEMO_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <typename F>
+nemo_status guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return NEMO_OK;
+  } catch (const NemoError& e) {
+    g_last_error = e.what();
+    return e.status;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return NEMO_ERR_OOM;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return NEMO_ERR_INVALID;
+  }
+}
+
+// Device allocation owned by a unique_ptr.
+struct DevFree {
+  void operator()(void* p) const {
+    if (p) (void)hipFree(p);
+  }
+};
+using DevPtr = std::unique_ptr<void, DevFree>;
+
+DevPtr dev_alloc(size_t bytes, const char* what) {
+  void* p = nullptr;
+  if (bytes == 0) bytes = 16;
+  hip_check(hipMalloc(&p, bytes), what);
+  return DevPtr(p);
+}
+
+struct DevTensor {
+  int type = -1;
+  std::vector<int64_t> dims;
+  DevPtr data;   // raw bytes (Q6_K: 208-byte records)
+  DevPtr d6;     // Q6_K matrices: per-block f16 scale (null when stored raw)
+  size_t bytes = 0;  // GGUF byte size
+};
+
+size_t ggml_bytes(int type, const std::vector<int64_t>& dims) {
+  int64_t n = 1;
+  for (int64_t d : dims) {
+    if (d <= 0) fail(NEMO_ERR_INVALID, "tensor dimensions must be positive");
+    n *= d;
+  }
+  switch (type) {
+    case kF32: return (size_t)n * 4;
+    case kF16: return (size_t)n * 2;
+    case kQ4_0:
+      if (dims[0] % 32) fail(NEMO_ERR_INVALID, "Q4_0 row length must be a multiple of 32");
+      return (size_t)(n / 32) * 18;
+    case kQ4_K:
+    case kQ6_K:
+      if (dims[0] % 256) fail(NEMO_ERR_INVALID, "K-quant row length must be a multiple of 256");
+      return (size_t)(n / 256) * (type == kQ4_K ? 144 : 210);
+    default: fail(NEMO_ERR_UNSUPPORTED, "unsupported GGML type " + std::to_string(type));
+  }
+}
+
+// Split raw Q6_K blocks into 208-byte records + f16 scales (see QWeight).
+void split_q6k(const uint8_t* raw, int64_t nb, std::vector<uint8_t>& rec, std::vector<uint16_t>& d) {
+  rec.resize((size_t)nb * 208);
+  d.resize((size_t)nb);
+  for (int64_t b = 0; b < nb; ++b) {
+    memcpy(rec.data() + b * 208, raw + b * 210, 208);
+    d[b] = (uint16_t)(raw[b * 210 + 208] | (raw[b * 210 + 209] << 8));
+  }
+}
+
+void upload_tensor(DevTensor& t, int type, const std::vector<int64_t>& dims, const void* bytes, size_t n_bytes,
+                   const std::string& name) {
+  const size_t expect = ggml_bytes(type, dims);
+  if (n_bytes != expect)
+    fail(NEMO_ERR_INVALID, name + " has " + std::to_string(n_bytes) + " bytes; expected " + std::to_string(expect));
+  t.type = type;
+  t.dims = dims;
+  t.bytes = n_bytes;
+  // Q6_K matrices are split for aligned GEMM loads; the Q6_K token table
+  // stays in its raw 210-byte rows (read by the embedding lookup).
+  if (type == kQ6_K && name != "token_embd.weight") {
+    std::vector<uint8_t> rec;
+    std::vector<uint16_t> d;
+    const int64_t nb = (int64_t)(n_bytes / 210);
+    split_q6k((const uint8_t*)bytes, nb, rec, d);
+    t.data = dev_alloc(rec.size(), "Q6_K records");
+    t.d6 = dev_alloc(d.size() * 2, "Q6_K scales");
+    hip_check(hipMemcpy(t.data.get(), rec.data(), rec.size(), hipMemcpyHostToDevice), "upload");
+    hip_check(hipMemcpy(t.d6.get(), d.data(), d.size() * 2, hipMemcpyHostToDevice), "upload");
+  } else {
+    t.data = dev_alloc(n_bytes, name.c_str());
+    hip_check(hipMemcpy(t.data.get(), bytes, n_bytes, hipMemcpyHostToDevice), "upload");
+  }
+}
+
+QWeight as_qweight(const DevTensor& t) {
+  QWeight w;
+  w.type = t.type;
+  w.k = (int)t.dims[0];
+  w.n = (int)t.dims[1];
+  w.blocks = (const uint8_t*)t.data.get();
+  w.d = (const uint16_t*)t.d6.get();
+  return w;
+}
+
+int merged_length(int sequence) {  // contextualMergedLength, src/webgpu/model.ts:30-32
+  const double m = ceil((double)sequence * 0.64);
+  return m < 1 ? 1 : (int)m;
+}
+
+// Stage names of profile() (src/webgpu/model.ts:198-211).
+const char* const kStages[] = {"embedding_norm", "token_merge", "qkv", "rope_attention", "attention_output",
+                               "post_attention_norm", "ffn_up_gate", "swiglu", "ffn_down", "post_ffn_norm", "pool"};
+constexpr int kNumStages = 11;
+
+}  // namespace
+
+struct nemo_ctx {
+  int device = 0;
+};
+
+struct LayerWeights {
+  QWeight qkv, o, gate_up, down;
+  const float* attn_norm = nullptr;
+  const float* ffn_norm = nullptr;
+};
+
+struct nemo_model {
+  nemo_ctx* ctx = nullptr;
+  nemo_dims dims{};
+  std::map<std::string, DevTensor> tensors;
+  bool finalized = false;
+  std::vector<LayerWeights> layers;
+  const float* output_norm = nullptr;
+  int embedding_type = -1;
+  const void* embedding = nullptr;
+  int live_plans = 0;
+};
+
+struct nemo_weight {
+  nemo_ctx* ctx = nullptr;
+  DevTensor t;
+  QWeight w{};
+  DevPtr partials;
+};
+
+struct nemo_plan {
+  nemo_model* model = nullptr;
+  int batch = 0, sequence = 0, merged = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, gate_up, ffn, out, rope;
+  uint32_t* h_ids = nullptr;   // pinned staging
+  float* h_out = nullptr;
+  ~nemo_plan() {
+    if (h_ids) (void)hipHostFree(h_ids);
+    if (h_out) (void)hipHostFree(h_out);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+static void set_device(nemo_ctx* ctx) { hip_check(hipSetDevice(ctx->device), "hipSetDevice"); }
+
+static void validate_dims(const nemo_dims& d) {
+  if (d.hidden <= 0 || d.hidden % 256) fail(NEMO_ERR_INVALID, "hidden must be a positive multiple of 256");
+  if (d.q_heads <= 0 || d.kv_heads <= 0 || d.q_heads % d.kv_heads)
+    fail(NEMO_ERR_INVALID, "q_heads must be a positive multiple of kv_heads");
+  if (d.head_dim != 64 && d.head_dim != 128) fail(NEMO_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+  if ((d.q_heads * d.head_dim) % 256) fail(NEMO_ERR_INVALID, "q_heads * head_dim must be a multiple of 256");
+  if (d.intermediate <= 0 || d.intermediate % 256) fail(NEMO_ERR_INVALID, "intermediate must be a multiple of 256");
+  if (d.layers <= 0 || d.merge_after_layer < 0 || d.merge_after_layer > d.layers)
+    fail(NEMO_ERR_INVALID, "merge_after_layer must lie in [0, layers]");
+  if (d.vocab <= 0) fail(NEMO_ERR_INVALID, "vocab must be positive");
+  if (d.kv_stride < 1) fail(NEMO_ERR_INVALID, "kv_stride must be >= 1");
+}
+
+// Every nemo_* definition below takes C linkage from its declaration in nemo.h.
+
+void nemo_dims_reference(nemo_dims* out) {
+  if (!out) return;
+  out->hidden = 2048;
+  out->q_heads = 24;
+  out->kv_heads = 8;
+  out->head_dim = 128;
+  out->intermediate = 6144;
+  out->layers = 16;
+  out->vocab = 131072;
+  out->merge_after_layer = 4;
+  out->rms_epsilon = 1e-5f;
+  out->rope_theta = 1e6f;
+  out->kv_stride_threshold = 2048;
+  out->kv_stride = 3;
+}
+
+const char* nemo_last_error(void) { return g_last_error.c_str(); }
+
+const char* nemo_version(void) { return "libnemo 0.1 gfx950"; }
+
+nemo_status nemo_init(int32_t device, nemo_ctx** out) {
+  return guarded([&] {
+    if (!out) fail(NEMO_ERR_INVALID, "out is null");
+    int count = 0;
+    hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+      fail(NEMO_ERR_INVALID, "device " + std::to_string(device) + " out of range (" + std::to_string(count) + ")");
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    auto* c = new nemo_ctx;
+    c->device = device;
+    *out = c;
+  });
+}
+
+nemo_status nemo_shutdown(nemo_ctx* ctx) {
+  return guarded([&] { delete ctx; });
+}
+
+nemo_status nemo_model_create(nemo_ctx* ctx, const nemo_dims* dims, nemo_model** out) {
+  return guarded([&] {
+    if (!ctx || !dims || !out) fail(NEMO_ERR_INVALID, "null argument");
+    validate_dims(*dims);
+    auto* m = new nemo_model;
+    m->ctx = ctx;
+    m->dims = *dims;
+    *out = m;
+  });
+}
+
+nemo_status nemo_model_set_tensor(nemo_model* model, const char* name, int32_t ggml_type, const int64_t* dims,
+                                  int32_t n_dims, const void* bytes, size_t n_bytes) {
+  return guarded([&] {
+    if (!model || !name || !dims || n_dims <= 0 || n_dims > 4 || (!bytes && n_bytes))
+      fail(NEMO_ERR_INVALID, "invalid tensor arguments");
+    if (model->finalized) fail(NEMO_ERR_INVALID, "model is finalized");
+    set_device(model->ctx);
+    DevTensor t;
+    upload_tensor(t, ggml_type, std::vector<int64_t>(dims, dims + n_dims), bytes, n_bytes, name);
+    model->tensors[name] = std::move(t);
+  });
+}
+
+static DevTensor synth_matrix(int type, int64_t k, int64_t n, uint64_t key, hipStream_t s) {
+  DevTensor t;
+  t.type = type;
+  t.dims = {k, n};
+  t.bytes = ggml_bytes(type, t.dims);
+  const int64_t nb = k / 256 * n;
+  if (type == kQ4_K) {
+    t.data = dev_alloc(t.bytes, "synthetic Q4_K");
+    hip_check(launch_synth_q4k(key, 0.02f, nb, (uint8_t*)t.data.get(), s), "synthesize");
+  } else {
+    t.data = dev_alloc((size_t)nb * 208, "synthetic Q6_K");
+    t.d6 = dev_alloc((size_t)nb * 2, "synthetic Q6_K scales");
+    hip_check(launch_synth_q6k(key, 0.02f, nb, (uint8_t*)t.data.get(), (uint16_t*)t.d6.get(), s), "synthesize");
+  }
+  return t;
+}
+
+static DevTensor ones_vector(int64_t n, hipStream_t s) {
+  DevTensor t;
+  t.type = kF32;
+  t.dims = {n};
+  t.bytes = (size_t)n * 4;
+  t.data = dev_alloc(t.bytes, "norm weight");
+  hip_check(launch_fill_f32(1.0f, n, (float*)t.data.get(), s), "synthesize");
+  return t;
+}
+
+nemo_status nemo_model_synthesize(nemo_model* model, uint64_t seed, int32_t embedding_type) {
+  return guarded([&] {
+    if (!model) fail(NEMO_ERR_INVALID, "model is null");
+    if (model->finalized) fail(NEMO_ERR_INVALID, "model is finalized");
+    if (embedding_type != kF16 && embedding_type != kQ6_K)
+      fail(NEMO_ERR_INVALID, "embedding type must be F16 or Q6_K");
+    set_device(model->ctx);
+    const nemo_dims& d = model->dims;
+    const int64_t H = d.hidden, QKV = (int64_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+    const int64_t QW = (int64_t)d.q_heads * d.head_dim, F = d.intermediate;
+    hipStream_t s = nullptr;
+    for (int l = 0; l < d.layers; ++l) {
+      const std::string p = "blk." + std::to_string(l) + ".";
+      model->tensors[p + "attn_qkv.weight"] = synth_matrix(kQ4_K, H, QKV, synth_key(seed, 16 * l + 0), s);
+      model->tensors[p + "attn_output.weight"] = synth_matrix(kQ4_K, QW, H, synth_key(seed, 16 * l + 1), s);
+      model->tensors[p + "ffn_gate_up.weight"] = synth_matrix(kQ4_K, H, 2 * F, synth_key(seed, 16 * l + 2), s);
+      model->tensors[p + "ffn_down.weight"] = synth_matrix(kQ6_K, F, H, synth_key(seed, 16 * l + 3), s);
+      model->tensors[p + "attn_norm.weight"] = ones_vector(H, s);
+      model->tensors[p + "ffn_norm.weight"] = ones_vector(H, s);
+    }
+    model->tensors["output_norm.weight"] = ones_vector(H, s);
+    DevTensor e;
+    e.type = embedding_type;
+    e.dims = {H, (int64_t)d.vocab};
+    e.bytes = ggml_bytes(embedding_type, e.dims);
+    const uint64_t ekey = synth_key(seed, 1u << 20);
+    if (embedding_type == kF16) {
+      e.data = dev_alloc(e.bytes, "synthetic embedding");
+      hip_check(launch_synth_f16(ekey, 0.02f, H * d.vocab, (uint16_t*)e.data.get(), s), "synthesize");
+    } else {
+      // Q6_K table rows are read raw (210-byte blocks) by the lookup kernel:
+      // synthesize split records, then interleave on the host.
+      DevTensor tmp = synth_matrix(kQ6_K, H, d.vocab, ekey, s);
+      hip_check(hipDeviceSynchronize(), "synthesize");
+      const int64_t nb = H / 256 * d.vocab;
+      std::vector<uint8_t> rec((size_t)nb * 208), raw((size_t)nb * 210);
+      std::vector<uint16_t> dd((size_t)nb);
+      hip_check(hipMemcpy(rec.data(), tmp.data.get(), rec.size(), hipMemcpyDeviceToHost), "synthesize");
+      hip_check(hipMemcpy(dd.data(), tmp.d6.get(), dd.size() * 2, hipMemcpyDeviceToHost), "synthesize");
+      for (int64_t b = 0; b < nb; ++b) {
+        memcpy(raw.data() + b * 210, rec.data() + b * 208, 208);
+        raw[b * 210 + 208] = (uint8_t)(dd[b] & 0xff);
+        raw[b * 210 + 209] = (uint8_t)(dd[b] >> 8);
+      }
+      e.data = dev_alloc(e.bytes, "synthetic embedding");
+      hip_check(hipMemcpy(e.data.get(), raw.data(), raw.size(), hipMemcpyHostToDevice), "synthesize");
+    }
+    model->tensors["token_embd.weight"] = std::move(e);
+    hip_check(hipDeviceSynchronize(), "synthesize");
+  });
+}
+
+static const DevTensor& need(nemo_model* m, const std::string& name) {
+  auto it = m->tensors.find(name);
+  if (it == m->tensors.end()) fail(NEMO_ERR_MISSING, "missing tensor " + name);
+  return it->second;
+}
+
+// Concatenate matrices by rows (combineQ4, src/webgpu/model.ts:288-300).
+static void fuse_rows(nemo_model* m, const std::string& name, const std::vector<std::string>& parts) {
+  if (m->tensors.count(name)) return;
+  std::vector<const DevTensor*> src;
+  for (const auto& p : parts) {
+    auto it = m->tensors.find(p);
+    if (it == m->tensors.end()) fail(NEMO_ERR_MISSING, "missing tensor " + name + " (or its part " + p + ")");
+    src.push_back(&it->second);
+  }
+  const DevTensor& first = *src[0];
+  int64_t rows = 0;
+  for (auto* t : src) {
+    if (t->type != first.type || (t->type != kQ4_K && t->type != kQ6_K) || t->dims.size() != 2 ||
+        t->dims[0] != first.dims[0]) {
+      std::string all;
+      for (const auto& p : parts) all += (all.empty() ? "" : ", ") + p;
+      fail(NEMO_ERR_INVALID, "cannot combine " + all);
+    }
+    rows += t->dims[1];
+  }
+  DevTensor f;
+  f.type = first.type;
+  f.dims = {first.dims[0], rows};
+  f.bytes = ggml_bytes(f.type, f.dims);
+  const size_t row_bytes = qweight_row_bytes(f.type, (int)first.dims[0]);
+  f.data = dev_alloc(row_bytes * rows, "fused matrix");
+  if (f.type == kQ6_K) f.d6 = dev_alloc((size_t)(first.dims[0] / 256) * rows * 2, "fused scales");
+  size_t off = 0, doff = 0;
+  for (auto* t : src) {
+    const size_t bytes = row_bytes * t->dims[1];
+    hip_check(hipMemcpy((uint8_t*)f.data.get() + off, t->data.get(), bytes, hipMemcpyDeviceToDevice), "fuse");
+    off += bytes;
+    if (f.type == kQ6_K) {
+      const size_t db = (size_t)(first.dims[0] / 256) * t->dims[1] * 2;
+      hip_check(hipMemcpy((uint8_t*)f.d6.get() + doff, t->d6.get(), db, hipMemcpyDeviceToDevice), "fuse");
+      doff += db;
+    }
+  }
+  m->tensors[name] = std::move(f);
+  for (const auto& p : parts) m->tensors.erase(p);
+}
+
+static QWeight matrix(nemo_model* m, const std::string& name, int64_t k, int64_t n) {
+  const DevTensor& t = need(m, name);
+  if (t.dims.size() != 2) fail(NEMO_ERR_INVALID, "invalid matrix " + name);
+  if (t.type != kQ4_K && t.type != kQ6_K)
+    fail(NEMO_ERR_UNSUPPORTED, "unsupported matrix type " + std::to_string(t.type) + " for " + name);
+  if (t.dims[0] != k || t.dims[1] != n)
+    fail(NEMO_ERR_INVALID, name + " has dims [" + std::to_string(t.dims[0]) + ", " + std::to_string(t.dims[1]) +
+                               "]; expected [" + std::to_string(k) + ", " + std::to_string(n) + "]");
+  return as_qweight(t);
+}
+
+static const float* vec_f32(nemo_model* m, const std::string& name, int64_t n) {
+  const DevTensor& t = need(m, name);
+  if (t.type != kF32 || t.dims.size() != 1 || t.dims[0] != n)
+    fail(NEMO_ERR_INVALID, name + " must be F32 [" + std::to_string(n) + "]");
+  return (const float*)t.data.get();
+}
+
+nemo_status nemo_model_finalize(nemo_model* model) {
+  return guarded([&] {
+    if (!model) fail(NEMO_ERR_INVALID, "model is null");
+    if (model->finalized) return;
+    set_device(model->ctx);
+    const nemo_dims& d = model->dims;
+    const int64_t H = d.hidden, QKV = (int64_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+    const int64_t QW = (int64_t)d.q_heads * d.head_dim, F = d.intermediate;
+    std::vector<LayerWeights> layers(d.layers);
+    for (int l = 0; l < d.layers; ++l) {
+      const std::string p = "blk." + std::to_string(l) + ".";
+      fuse_rows(model, p + "attn_qkv.weight", {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"});
+      fuse_rows(model, p + "ffn_gate_up.weight", {p + "ffn_gate.weight", p + "ffn_up.weight"});
+      layers[l].qkv = matrix(model, p + "attn_qkv.weight", H, QKV);
+      layers[l].o = matrix(model, p + "attn_output.weight", QW, H);
+      layers[l].gate_up = matrix(model, p + "ffn_gate_up.weight", H, 2 * F);
+      layers[l].down = matrix(model, p + "ffn_down.weight", F, H);
+      layers[l].attn_norm = vec_f32(model, p + "attn_norm.weight", H);
+      layers[l].ffn_norm = vec_f32(model, p + "ffn_norm.weight", H);
+    }
+    model->output_norm = vec_f32(model, "output_norm.weight", H);
+    const DevTensor& e = need(model, "token_embd.weight");
+    if ((e.type != kF16 && e.type != kQ6_K) || e.dims.size() != 2 || e.dims[0] != H || e.dims[1] != d.vocab)
+      fail(NEMO_ERR_INVALID, "token_embd.weight must be F16 or Q6_K [" + std::to_string(H) + ", " +
+                                 std::to_string(d.vocab) + "]");
+    model->embedding_type = e.type;
+    model->embedding = e.data.get();
+    model->layers = std::move(layers);
+    model->finalized = true;
+  });
+}
+
+nemo_status nemo_model_get_tensor(nemo_model* model, const char* name, int32_t* ggml_type, int64_t* dims4, void* out,
+                                  size_t* n_bytes) {
+  return guarded([&] {
+    if (!model || !name || !n_bytes) fail(NEMO_ERR_INVALID, "null argument");
+    set_device(model->ctx);
+    const DevTensor& t = need(model, name);
+    if (ggml_type) *ggml_type = t.type;
+    if (dims4)
+      for (int i = 0; i < 4; ++i) dims4[i] = i < (int)t.dims.size() ? t.dims[i] : 1;
+    if (!out) {
+      *n_bytes = t.bytes;
+      return;
+    }
+    if (*n_bytes < t.bytes) fail(NEMO_ERR_INVALID, "output buffer too small");
+    hip_check(hipDeviceSynchronize(), "sync");
+    if (t.type == kQ6_K && t.d6) {
+      const int64_t nb = (int64_t)(t.bytes / 210);
+      std::vector<uint8_t> rec((size_t)nb * 208);
+      std::vector<uint16_t> dd((size_t)nb);
+      hip_check(hipMemcpy(rec.data(), t.data.get(), rec.size(), hipMemcpyDeviceToHost), "download");
+      hip_check(hipMemcpy(dd.data(), t.d6.get(), dd.size() * 2, hipMemcpyDeviceToHost), "download");
+      uint8_t* o = (uint8_t*)out;
+      for (int64_t b = 0; b < nb; ++b) {
+        memcpy(o + b * 210, rec.data() + b * 208, 208);
+        o[b * 210 + 208] = (uint8_t)(dd[b] & 0xff);
+        o[b * 210 + 209] = (uint8_t)(dd[b] >> 8);
+      }
+    } else {
+      hip_check(hipMemcpy(out, t.data.get(), t.bytes, hipMemcpyDeviceToHost), "download");
+    }
+    *n_bytes = t.bytes;
+  });
+}
+
+nemo_status nemo_model_destroy(nemo_model* model) {
+  return guarded([&] {
+    if (!model) return;
+    if (model->live_plans) fail(NEMO_ERR_INVALID, "model still has live plans");
+    set_device(model->ctx);
+    delete model;
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Plan
+// ---------------------------------------------------------------------------
+
+// RoPE table (src/webgpu/model.ts:95-106), computed in double, stored float:
+// [sequence][head_dim/2] pairs of (cos, sin).
+static std::vector<float> rope_table(int sequence, int head_dim, double theta) {
+  const int pairs = head_dim / 2;
+  const double pi = 3.14159265358979323846;
+  auto correction = [&](double beta) { return head_dim * log(16384.0 / (beta * 2 * pi)) / (2 * log(theta)); };
+  const double lo = floor(correction(32)), hi = ceil(correction(1));
+  std::vector<float> v((size_t)sequence * pairs * 2);
+  for (int p = 0; p < sequence; ++p)
+    for (int i = 0; i < pairs; ++i) {
+      const double ramp = 1 - fmin(1.0, fmax(0.0, (i - lo) / fmax(0.001, hi - lo)));
+      const double freq = (1.0 / 16) * (1 - ramp) + ramp;
+      const double angle = p * pow(theta, -(double)i / pairs) * freq;
+      v[((size_t)p * pairs + i) * 2] = (float)cos(angle);
+      v[((size_t)p * pairs + i) * 2 + 1] = (float)sin(angle);
+    }
+  return v;
+}
+
+nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence, nemo_plan** out) {
+  return guarded([&] {
+    if (!model || !out) fail(NEMO_ERR_INVALID, "null argument");
+    if (!model->finalized) fail(NEMO_ERR_INVALID, "model is not finalized");
+    if (batch < 1 || batch > kMaxBatch) fail(NEMO_ERR_INVALID, "batch must be in [1, 64]");
+    if (sequence < 1) fail(NEMO_ERR_INVALID, "sequence must be >= 1");
+    set_device(model->ctx);
+    const nemo_dims& d = model->dims;
+    auto p = std::make_unique<nemo_plan>();
+    p->model = model;
+    p->batch = batch;
+    p->sequence = sequence;
+    p->merged = merged_length(sequence);
+    const size_t tf = (size_t)batch * sequence, tr = (size_t)batch * p->merged;
+    const size_t H = d.hidden, QKV = (size_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+    const size_t QW = (size_t)d.q_heads * d.head_dim, KW = (size_t)d.kv_heads * d.head_dim, F = d.intermediate;
+    hip_check(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking), "hipStreamCreate");
+    p->ids = dev_alloc(tf * 4, "token ids");
+    p->x_full = dev_alloc(tf * H * 2, "full residual stream");
+    p->norm_full = dev_alloc(tf * H * 2, "full normalized hidden state");
+    p->x_red = dev_alloc(tr * H * 2, "merged residual stream");
+    p->norm_red = dev_alloc(tr * H * 2, "merged normalized hidden state");
+    p->qkv = dev_alloc(tf * QKV * 2, "query + key + value raw");
+    p->q = dev_alloc(tf * QW * 2, "query rope");
+    p->k = dev_alloc(tf * KW * 2, "key rope");
+    p->attn = dev_alloc(tf * QW * 2, "attention");
+    p->delta = dev_alloc(tf * H * 2, "residual delta");
+    p->gate_up = dev_alloc(tf * 2 * F * 2, "FFN gate + up");
+    p->ffn = dev_alloc(tf * F * 2, "SwiGLU output");
+    p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
+    const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
+    p->rope = dev_alloc(table.size() * 4, "RoPE sin/cos table");
+    hip_check(hipMemcpy(p->rope.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "upload");
+    hip_check(hipHostMalloc((void**)&p->h_ids, tf * 4, hipHostMallocDefault), "pinned ids");
+    hip_check(hipHostMalloc((void**)&p->h_out, (size_t)batch * H * 4, hipHostMallocDefault), "pinned output");
+    model->live_plans++;
+    *out = p.release();
+  });
+}
+
+nemo_status nemo_plan_destroy(nemo_plan* plan) {
+  return guarded([&] {
+    if (!plan) return;
+    set_device(plan->model->ctx);
+    if (plan->stream) hip_check(hipStreamSynchronize(plan->stream), "sync");
+    plan->model->live_plans--;
+    delete plan;
+  });
+}
+
+nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, size_t* n_bytes) {
+  return guarded([&] {
+    if (!plan || !name || !n_bytes) fail(NEMO_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(plan->mu);
+    set_device(plan->model->ctx);
+    const nemo_dims& d = plan->model->dims;
+    const size_t tf = (size_t)plan->batch * plan->sequence, tr = (size_t)plan->batch * plan->merged;
+    const size_t H = d.hidden, QKV = (size_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+    const size_t QW = (size_t)d.q_heads * d.head_dim, KW = (size_t)d.kv_heads * d.head_dim, F = d.intermediate;
+    const std::string n = name;
+    const void* src = nullptr;
+    size_t bytes = 0;
+    if (n == "x_full") src = plan->x_full.get(), bytes = tf * H * 2;
+    else if (n == "norm_full") src = plan->norm_full.get(), bytes = tf * H * 2;
+    else if (n == "x_merged") src = plan->x_red.get(), bytes = tr * H * 2;
+    else if (n == "norm_merged") src = plan->norm_red.get(), bytes = tr * H * 2;
+    else if (n == "qkv") src = plan->qkv.get(), bytes = tf * QKV * 2;
+    else if (n == "q") src = plan->q.get(), bytes = tf * QW * 2;
+    else if (n == "k") src = plan->k.get(), bytes = tf * KW * 2;
+    else if (n == "attention") src = plan->attn.get(), bytes = tf * QW * 2;
+    else if (n == "delta") src = plan->delta.get(), bytes = tf * H * 2;
+    else if (n == "gate_up") src = plan->gate_up.get(), bytes = tf * 2 * F * 2;
+    else if (n == "ffn") src = plan->ffn.get(), bytes = tf * F * 2;
+    else if (n == "embeddings") src = plan->out.get(), bytes = (size_t)plan->batch * H * 4;
+    else fail(NEMO_ERR_INVALID, "unknown plan buffer " + n);
+    if (!out) {
+      *n_bytes = bytes;
+      return;
+    }
+    if (*n_bytes < bytes) fail(NEMO_ERR_INVALID, "output buffer too small");
+    hip_check(hipStreamSynchronize(plan->stream), "sync");
+    hip_check(hipDeviceSynchronize(), "sync");
+    hip_check(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost), "download");
+    *n_bytes = bytes;
+  });
+}
+
+int32_t nemo_profile_stage_count(void) { return kNumStages; }
+
+const char* nemo_profile_stage_name(int32_t index) {
+  return index >= 0 && index < kNumStages ? kStages[index] : "";
+}
+
+// Ragged tables of one run: lengths -> source rows; targetLengths
+// (src/webgpu/model.ts:226-233) -> merged rows.
+static void ragged_tables(nemo_plan* p, const uint32_t* lengths, size_t n_lengths, Ragged& src, Ragged& dst) {
+  if (!lengths) fail(NEMO_ERR_INVALID, "lengths is null");
+  if ((int)n_lengths != p->batch) fail(NEMO_ERR_INVALID, "lengths do not match execution plan");
+  src.count = dst.count = p->batch;
+  src.start[0] = dst.start[0] = 0;
+  for (int b = 0; b < p->batch; ++b) {
+    const uint32_t len = lengths[b];
+    if (len < 1 || len > (uint32_t)p->sequence)
+      fail(NEMO_ERR_INVALID, "lengths[" + std::to_string(b) + "] = " + std::to_string(len) + " outside [1, " +
+                                 std::to_string(p->sequence) + "]");
+    src.start[b + 1] = src.start[b] + (int)len;
+    dst.start[b + 1] = dst.start[b] + std::min(p->merged, merged_length((int)len));
+  }
+}
+
+// Enqueue the whole graph (src/webgpu/model.ts:154-168). `mark(stage, begin)`
+// brackets stages for profiling.
+template <typename Mark>
+static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src, const Ragged& dst, float* d_out,
+                          hipStream_t s, Mark&& mark) {
+  nemo_model* m = p->model;
+  const nemo_dims& d = m->dims;
+  const int H = d.hidden, QKV = (d.q_heads + 2 * d.kv_heads) * d.head_dim, QW = d.q_heads * d.head_dim;
+  const int F = d.intermediate;
+  uint16_t* x_full = (uint16_t*)p->x_full.get();
+  uint16_t* norm_full = (uint16_t*)p->norm_full.get();
+  uint16_t* x_red = (uint16_t*)p->x_red.get();
+  uint16_t* norm_red = (uint16_t*)p->norm_red.get();
+  uint16_t* qkv = (uint16_t*)p->qkv.get();
+  uint16_t* q = (uint16_t*)p->q.get();
+  uint16_t* k = (uint16_t*)p->k.get();
+  uint16_t* attn = (uint16_t*)p->attn.get();
+  uint16_t* delta = (uint16_t*)p->delta.get();
+  uint16_t* gu = (uint16_t*)p->gate_up.get();
+  uint16_t* ffn = (uint16_t*)p->ffn.get();
+  const float* rope = (const float*)p->rope.get();
+
+  mark(0, true);
+  hip_check(launch_embed(d_ids, p->sequence, src, m->embedding_type, m->embedding, H, d.vocab, x_full, s), "embedding");
+  hip_check(launch_rmsnorm(x_full, nullptr, m->layers[0].attn_norm, norm_full, src.start[src.count], H, d.rms_epsilon, s),
+            "rmsnorm");
+  mark(0, false);
+  for (int l = 0; l < d.layers; ++l) {
+    if (l == d.merge_after_layer) {
+      mark(1, true);
+      hip_check(launch_merge(x_full, src, dst, H, x_red, s), "token merge");
+      hip_check(launch_merge(norm_full, src, dst, H, norm_red, s), "token merge");
+      mark(1, false);
+    }
+    const bool full = l < d.merge_after_layer;
+    const Ragged& rows = full ? src : dst;
+    const int M = rows.start[rows.count];
+    uint16_t* x = full ? x_full : x_red;
+    uint16_t* norm = full ? norm_full : norm_red;
+    const LayerWeights& w = m->layers[l];
+    mark(2, true);
+    hip_check(launch_gemm(norm, H, w.qkv, qkv, QKV, M, s), "qkv matmul");
+    mark(2, false);
+    mark(3, true);
+    hip_check(launch_rope(qkv, QKV, rows, rope, d.q_heads, d.kv_heads, d.head_dim, q, k, s), "rope");
+    hip_check(launch_attention(q, k, qkv + (size_t)(d.q_heads + d.kv_heads) * d.head_dim, QKV, rows, d.q_heads,
+                               d.kv_heads, d.head_dim, d.kv_stride_threshold, d.kv_stride, attn, s),
+              "attention");
+    mark(3, false);
+    mark(4, true);
+    hip_check(launch_gemm(attn, QW, w.o, delta, H, M, s), "attention output matmul");
+    mark(4, false);
+    mark(5, true);
+    hip_check(launch_rmsnorm(x, delta, w.ffn_norm, norm, M, H, d.rms_epsilon, s), "rmsnorm");
+    mark(5, false);
+    mark(6, true);
+    hip_check(launch_gemm(norm, H, w.gate_up, gu, 2 * F, M, s), "gate/up matmul");
+    mark(6, false);
+    mark(7, true);
+    hip_check(launch_swiglu(gu, M, F, ffn, s), "swiglu");
+    mark(7, false);
+    mark(8, true);
+    hip_check(launch_gemm(ffn, F, w.down, delta, H, M, s), "down matmul");
+    mark(8, false);
+    mark(9, true);
+    const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
+    hip_check(launch_rmsnorm(x, delta, next, norm, M, H, d.rms_epsilon, s), "rmsnorm");
+    mark(9, false);
+  }
+  if (d.merge_after_layer == d.layers) {  // merge after the last layer (models shorter than the reference)
+    mark(1, true);
+    hip_check(launch_merge(norm_full, src, dst, H, norm_red, s), "token merge");
+    mark(1, false);
+  }
+  mark(10, true);
+  hip_check(launch_mean_pool(norm_red, dst, H, d_out, s), "mean pool");
+  mark(10, false);
+}
+
+static void check_ids_host(nemo_plan* p, const uint32_t* ids, size_t n_ids, const Ragged& src) {
+  if (!ids) fail(NEMO_ERR_INVALID, "ids is null");
+  if (n_ids != (size_t)p->batch * p->sequence) fail(NEMO_ERR_INVALID, "token buffer does not match execution plan");
+  const uint32_t vocab = (uint32_t)p->model->dims.vocab;
+  for (int b = 0; b < p->batch; ++b)
+    for (int t = 0; t < src.start[b + 1] - src.start[b]; ++t)
+      if (ids[(size_t)b * p->sequence + t] >= vocab)
+        fail(NEMO_ERR_INVALID, "token id " + std::to_string(ids[(size_t)b * p->sequence + t]) + " outside vocabulary");
+}
+
+nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, const uint32_t* lengths,
+                          size_t n_lengths, float* out) {
+  return guarded([&] {
+    if (!plan || !out) fail(NEMO_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(plan->mu);
+    set_device(plan->model->ctx);
+    Ragged src, dst;
+    ragged_tables(plan, lengths, n_lengths, src, dst);
+    check_ids_host(plan, ids, n_ids, src);
+    const size_t H = plan->model->dims.hidden;
+    hipStream_t s = plan->stream;
+    memcpy(plan->h_ids, ids, n_ids * 4);
+    hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
+    enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s, [](int, bool) {});
+    hip_check(hipMemcpyAsync(plan->h_out, plan->out.get(), (size_t)plan->batch * H * 4, hipMemcpyDeviceToHost, s),
+              "readback");
+    hip_check(hipStreamSynchronize(s), "run");
+    memcpy(out, plan->h_out, (size_t)plan->batch * H * 4);
+  });
+}
+
+nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const uint32_t* lengths, size_t n_lengths,
+                                 float* d_out, void* stream) {
+  return guarded([&] {
+    if (!plan || !d_ids || !d_out) fail(NEMO_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(plan->mu);
+    set_device(plan->model->ctx);
+    Ragged src, dst;
+    ragged_tables(plan, lengths, n_lengths, src, dst);
+    hipStream_t s = stream ? (hipStream_t)stream : plan->stream;
+    enqueue_graph(plan, d_ids, src, dst, d_out, s, [](int, bool) {});
+  });
+}
+
+nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids, const uint32_t* lengths,
+                              size_t n_lengths, float* stage_ms, int32_t n_stages) {
+  return guarded([&] {
+    if (!plan || !stage_ms || n_stages < kNumStages) fail(NEMO_ERR_INVALID, "stage_ms needs 11 entries");
+    std::lock_guard<std::mutex> lock(plan->mu);
+    set_device(plan->model->ctx);
+    Ragged src, dst;
+    ragged_tables(plan, lengths, n_lengths, src, dst);
+    check_ids_host(plan, ids, n_ids, src);
+    hipStream_t s = plan->stream;
+    memcpy(plan->h_ids, ids, n_ids * 4);
+    hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
+    // One event pair per stage instance, like the reference's one timestamp
+    // pair per compute pass.
+    const int instances = 3 + plan->model->dims.layers * 8;
+    std::vector<hipEvent_t> events(2 * instances);
+    for (auto& e : events) hip_check(hipEventCreate(&e), "hipEventCreate");
+    std::vector<int> names;
+    int next = 0;
+    enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s,
+                  [&](int stage, bool begin) {
+                    if (begin) {
+                      names.push_back(stage);
+                      hip_check(hipEventRecord(events[2 * next], s), "hipEventRecord");
+                    } else {
+                      hip_check(hipEventRecord(events[2 * next + 1], s), "hipEventRecord");
+                      ++next;
+                    }
+                  });
+    hip_check(hipStreamSynchronize(s), "profile");
+    for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
+    for (int i = 0; i < next; ++i) {
+      float ms = 0.f;
+      hip_check(hipEventElapsedTime(&ms, events[2 * i], events[2 * i + 1]), "hipEventElapsedTime");
+      stage_ms[names[i]] += ms;
+    }
+    for (auto& e : events) (void)hipEventDestroy(e);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Kernel level
+// ---------------------------------------------------------------------------
+
+nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int32_t k, const void* bytes,
+                               size_t n_bytes, nemo_weight** out) {
+  return guarded([&] {
+    if (!ctx || !out || !bytes) fail(NEMO_ERR_INVALID, "null argument");
+    if (ggml_type != kQ4_K && ggml_type != kQ6_K) fail(NEMO_ERR_UNSUPPORTED, "weight type must be Q4_K or Q6_K");
+    if (k <= 0 || k % 256 != 0) fail(NEMO_ERR_INVALID, "quantized matmul K must be divisible by 256");
+    if (n <= 0) fail(NEMO_ERR_INVALID, "n must be positive");
+    set_device(ctx);
+    auto w = std::make_unique<nemo_weight>();
+    w->ctx = ctx;
+    upload_tensor(w->t, ggml_type, {k, n}, bytes, n_bytes, "weight");
+    w->w = as_qweight(w->t);
+    const size_t pf = gemv_partials_floats(w->w, 16);
+    if (pf) w->partials = dev_alloc(pf * 4, "GEMV partials");
+    *out = w.release();
+  });
+}
+
+nemo_status nemo_weight_destroy(nemo_weight* weight) {
+  return guarded([&] {
+    if (!weight) return;
+    set_device(weight->ctx);
+    hip_check(hipDeviceSynchronize(), "sync");
+    delete weight;
+  });
+}
+
+nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y, int32_t algo,
+                               void* stream) {
+  return guarded([&] {
+    if (!weight || !d_x || !d_y) fail(NEMO_ERR_INVALID, "null argument");
+    if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
+    set_device(weight->ctx);
+    hipStream_t s = (hipStream_t)stream;
+    const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= 16);
+    if (algo < 0 || algo > 2) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+    if (gemv) {
+      if (m > 16) fail(NEMO_ERR_INVALID, "GEMV takes m <= 16");
+      hip_check(launch_gemv(d_x, weight->w.k, weight->w, d_y, weight->w.n, m, (float*)weight->partials.get(), s),
+                "gemv");
+    } else {
+      hip_check(launch_gemm(d_x, weight->w.k, weight->w, d_y, weight->w.n, m, s), "gemm");
+    }
+  });
+}
+
+nemo_status nemo_weight_dequantize(nemo_weight* weight, float* d_out, void* stream) {
+  return guarded([&] {
+    if (!weight || !d_out) fail(NEMO_ERR_INVALID, "null argument");
+    set_device(weight->ctx);
+    hip_check(launch_dequant_weight(weight->w, d_out, (hipStream_t)stream), "dequantize");
+  });
+}
+
+nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_values, float* d_out_f32,
+                            uint16_t* d_out_f16, void* stream) {
+  return guarded([&] {
+    if (!d_raw || (!d_out_f32 && !d_out_f16)) fail(NEMO_ERR_INVALID, "null argument");
+    if (((uintptr_t)d_raw & 15) != 0) fail(NEMO_ERR_INVALID, "raw blocks must be 16-byte aligned");
+    const int per = ggml_type == kQ4_0 ? 32 : 256;
+    if (ggml_type != kQ4_K && ggml_type != kQ6_K && ggml_type != kQ4_0)
+      fail(NEMO_ERR_UNSUPPORTED, "dequantize supports Q4_0, Q4_K and Q6_K");
+    if (n_values < 0 || n_values % per) fail(NEMO_ERR_INVALID, "n_values is not a whole number of blocks");
+    hip_check(launch_dequant_raw(ggml_type, (const uint8_t*)d_raw, n_values / per, d_out_f32, d_out_f16,
+                                 (hipStream_t)stream),
+              "dequantize");
+  });
+}
+

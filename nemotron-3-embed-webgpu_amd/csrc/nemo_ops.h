@@ -1,0 +1,43 @@
+// Non-matmul kernels of the encoder pass (src/webgpu/ops.ts) on the ragged
+// packed token layout. Host-side launch helpers; kernels in nemo_ops.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nemo_common.h"
+
+namespace nemo {
+
+// x[t, :] = table row ids[b * padded_seq + p] for packed row t = (b, p).
+// table_type kF16 ([vocab, hidden] f16) or kQ6_K (raw GGUF rows).
+hipError_t launch_embed(const uint32_t* ids, int padded_seq, const Ragged& rows, int table_type, const void* table,
+                        int hidden, int vocab, uint16_t* x, hipStream_t stream);
+
+// normalized = f16(f32(x) * rsqrt(mean(v^2) + eps) * w); with delta != null,
+// v = f32(x) + f32(delta) is first stored into x (f16).
+hipError_t launch_rmsnorm(uint16_t* x, const uint16_t* delta, const float* w, uint16_t* normalized, int rows,
+                          int hidden, float eps, hipStream_t stream);
+
+// Rotate adjacent pairs of the query and key heads of qkv into q [t, Hq, hd]
+// and k [t, Hkv, hd]; position = row index within its request.
+hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, const float* table, int q_heads,
+                       int kv_heads, int head_dim, uint16_t* q, uint16_t* k, hipStream_t stream);
+
+// Bidirectional GQA attention per request; v rows are read from
+// v_base + t * v_stride + kv_head * head_dim.
+hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v_base, int v_stride,
+                            const Ragged& rows, int q_heads, int kv_heads, int head_dim, int stride_threshold,
+                            int key_stride, uint16_t* out, hipStream_t stream);
+
+// out[t, :F] = f16(silu(g) * u), g = gu[t, :F], u = gu[t, F:2F].
+hipError_t launch_swiglu(const uint16_t* gu, int rows, int f, uint16_t* out, hipStream_t stream);
+
+// Adjacent-state merge of every request from `src` rows to `dst` rows.
+hipError_t launch_merge(const uint16_t* in, const Ragged& src, const Ragged& dst, int hidden, uint16_t* out,
+                        hipStream_t stream);
+
+// Mean over each request's rows, then L2 normalise; out float [count, hidden].
+hipError_t launch_mean_pool(const uint16_t* norm, const Ragged& rows, int hidden, float* out, hipStream_t stream);
+
+}  // namespace nemo

@@ -1,0 +1,52 @@
+// Quantized-weight kernels of libnemo: GGML block decoding, the MFMA GEMM and
+// the small-M GEMV. Host-side launch helpers; kernels live in nemo_quant.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nemo {
+
+// GGML tensor type codes (src/gguf/types.ts:17-23).
+enum GgmlType : int { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_K = 12, kQ6_K = 14 };
+
+// A quantized weight matrix of n rows by k columns (GGUF dims [k, n]) as it
+// sits in device memory.
+//  Q4_K: `blocks` holds the GGUF bytes unchanged, 144-byte super-blocks, row
+//        major ((k / 256) blocks per row). Every block is 16-byte aligned.
+//  Q6_K: GGUF's 210-byte blocks are split at upload so that loads stay
+//        16-byte aligned: `blocks` holds 208-byte records (ql[128] qh[64]
+//        scales[16]) and `d` the per-block f16 scale, both row major.
+struct QWeight {
+  int type;
+  int n;
+  int k;
+  const uint8_t* blocks;
+  const uint16_t* d;
+};
+
+// Bytes per row of `blocks`.
+__host__ __device__ inline size_t qweight_row_bytes(int type, int k) {
+  return type == kQ4_K ? (size_t)(k / 256) * 144 : (size_t)(k / 256) * 208;
+}
+
+// Y[m, n] = f16( sum_k X[m, k] * W[n, k] ), fp32 accumulate. X is f16 with
+// row stride ldx, Y f16 with row stride ldy. Chooses the MFMA GEMM.
+hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
+                       hipStream_t stream);
+
+// Small-M path (m <= 16): split-K wavefront GEMV with a deterministic
+// reduction through `partials` (float, at least gemv_partials_floats()).
+size_t gemv_partials_floats(const QWeight& w, int m);
+hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
+                       float* partials, hipStream_t stream);
+
+// Decode raw GGUF blocks (Q4_K 144 B, Q6_K 210 B, Q4_0 18 B) to float32 and/or
+// f16 (either output may be null). n_blocks consecutive blocks.
+hipError_t launch_dequant_raw(int type, const uint8_t* raw, int64_t n_blocks, float* out_f32,
+                              uint16_t* out_f16, hipStream_t stream);
+
+// Decode an uploaded weight (any layout above) to float32 [n, k].
+hipError_t launch_dequant_weight(const QWeight& w, float* out_f32, hipStream_t stream);
+
+}  // namespace nemo

@@ -1,0 +1,102 @@
+"""End-to-end parity of the HIP encoder pass with the oracle's forward
+(src/webgpu/model.ts:146-176 restated in oracle/oracle.py), through the C ABI.
+
+Bar: cosine >= 0.9999 per embedding against the oracle (fp64 arithmetic, f16
+storage at the reference's points); |norm - 1| <= 0.01 (src/main.ts:218);
+a request's embedding is bit-identical whether it runs alone or inside a
+ragged batch (the reference accepts >= 0.999, src/main.ts:298).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import synth
+from nemo_amd import runtime as rt
+
+pytestmark = pytest.mark.gpu
+
+
+def _cos(a, b):
+    return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def _padded(seqs, seq_len, pad=11):
+    ids = np.full(len(seqs) * seq_len, pad, dtype=np.uint32)
+    for i, s in enumerate(seqs):
+        ids[i * seq_len:i * seq_len + len(s)] = s
+    return ids, np.array([len(s) for s in seqs], dtype=np.uint32)
+
+
+SMALL = [
+    # hidden, q_heads, kv_heads, head_dim, ffn, layers, vocab, merge_after, emb type, stride threshold
+    (256, 4, 2, 64, 512, 3, 600, 1, 1, 2048),
+    (256, 2, 1, 128, 768, 2, 500, 1, 14, 2048),
+    (512, 8, 2, 64, 1024, 3, 300, 2, 1, 24),      # stride-3 keys for requests longer than 24
+    (256, 4, 4, 64, 256, 1, 100, 1, 1, 2048),     # one layer, merge just before the pool
+]
+
+
+@pytest.mark.parametrize("cfg", SMALL)
+def test_forward_matches_oracle(torch_cuda, cfg):
+    H, Hq, Hkv, hd, F, L, V, merge_after, emb, thr = cfg
+    dims = rt.make_dims(hidden=H, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=F, layers=L, vocab=V,
+                        merge_after_layer=merge_after, kv_stride_threshold=thr)
+    tensors = synth.model_tensors(dims, seed=77 + H + L, embedding_type=emb, fused=(L != 2))
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    lengths = [5, 70, 1, 33, 64, 2]
+    seqs = [[1] + list(synth.randint(900 + i, n - 1, 2, V)) for i, n in enumerate(lengths)]
+    ids, lens = _padded(seqs, 70)
+    plan = model.createPlan(len(seqs), 70)
+    got = plan.run_sync(ids, lens)
+    for i, s in enumerate(seqs):
+        ref = oracle.forward_request(om, np.array(s))
+        c = _cos(got[i], ref)
+        assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
+        assert abs(np.linalg.norm(got[i]) - 1) <= 0.01
+    # batch composition invariance: each request alone gives the same bits.
+    for i, s in enumerate(seqs):
+        single = model.createPlan(1, len(s)).run_sync(np.array(s, dtype=np.uint32), [len(s)])[0]
+        assert np.array_equal(single.view(np.uint32), got[i].view(np.uint32)), f"request {i} differs alone"
+
+
+def test_plan_errors_mirror_reference(torch_cuda):
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=256, layers=1, vocab=50,
+                        merge_after_layer=1)
+    model = rt.NemotronHipModel(synth.model_tensors(dims, seed=3), dims=dims)
+    plan = model.createPlan(2, 8)
+    with pytest.raises(rt.NemoError, match="token buffer does not match execution plan"):
+        plan.run_sync(np.ones(15, dtype=np.uint32), [8, 8])
+    with pytest.raises(rt.NemoError, match="outside"):
+        plan.run_sync(np.ones(16, dtype=np.uint32), [9, 8])
+    with pytest.raises(rt.NemoError, match="outside vocabulary"):
+        plan.run_sync(np.full(16, 50, dtype=np.uint32), [8, 8])
+    out = plan.run_sync(np.ones(16, dtype=np.uint32), [8, 3])
+    assert len(out) == 2 and all(abs(np.linalg.norm(e) - 1) < 0.01 for e in out)
+
+
+def test_missing_tensor_is_named(torch_cuda):
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=256, layers=1, vocab=50,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=3)
+    del tensors["blk.0.ffn_norm.weight"]
+    with pytest.raises(rt.NemoError, match="missing tensor blk.0.ffn_norm.weight"):
+        rt.NemotronHipModel(tensors, dims=dims)
+
+
+def test_synthetic_model_readback_matches_oracle(torch_cuda):
+    """Device-synthesized weights read back through the ABI drive the oracle
+    to the same embedding (config dims, 2 layers, 40 tokens)."""
+    dims = rt.config_dims()
+    dims.layers, dims.merge_after_layer, dims.vocab = 2, 1, 4096
+    model = rt.NemotronHipModel(None, dims=dims, synthetic_seed=1003)
+    tensors = {}
+    for name in ["token_embd.weight", "output_norm.weight"] + [f"blk.{l}.{t}.weight" for l in range(2) for t in (
+            "attn_qkv", "attn_output", "ffn_gate_up", "ffn_down", "attn_norm", "ffn_norm")]:
+        typ, d, data = model.get_tensor(name)
+        tensors[name] = (typ, [x for x in d if x != 1] or [1], data)
+    om = synth.oracle_model(dims, tensors)
+    seq = [1] + list(synth.randint(5, 39, 2, dims.vocab))
+    got = model.createPlan(1, 40).run_sync(np.array(seq, dtype=np.uint32), [40])[0]
+    ref = oracle.forward_request(om, np.array(seq))
+    assert _cos(got, ref) >= 0.9999

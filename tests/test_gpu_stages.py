@@ -1,0 +1,54 @@
+"""Stage-wise parity of one encoder layer (the reference's one-layer shape:
+RMSNorm -> QKV -> RoPE -> attention -> O -> RMSNorm -> gate/up -> SwiGLU ->
+down -> RMSNorm) against the oracle's trace, buffer by buffer, through the
+C ABI's plan buffers. Bar per stage: relative Frobenius error <= 1e-2 (the
+projection bar of the build); the final embedding cosine >= 0.9999.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import synth
+from nemo_amd import runtime as rt
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("hd,emb", [(64, 1), (128, 1), (64, 14), (128, 14)])
+def test_one_layer_stages(torch_cuda, hd, emb):
+    H, F, V = 256, 512, 300
+    Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
+    dims = rt.make_dims(hidden=H, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=F, layers=1, vocab=V,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=500 + hd + emb, embedding_type=emb)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    n = 37
+    seq = np.array([1] + list(synth.randint(41, n - 1, 2, V)), dtype=np.uint32)
+    plan = model.createPlan(1, n)
+    got = plan.run_sync(seq, [n])[0]
+    trace = {}
+    ref = oracle.forward_request(om, seq.astype(np.int64), trace)
+    QKV = (Hq + 2 * Hkv) * hd
+    checks = {
+        "qkv": (plan.read_buffer("qkv")[: n * QKV], trace["qkv"][0]),
+        "q": (plan.read_buffer("q")[: n * Hq * hd], trace["q"][0]),
+        "k": (plan.read_buffer("k")[: n * Hkv * hd], trace["k"][0]),
+        "attention": (plan.read_buffer("attention")[: n * Hq * hd], trace["attention"][0]),
+        "gate_up": (plan.read_buffer("gate_up")[: n * 2 * F], trace["gate_up"][0]),
+        "ffn": (plan.read_buffer("ffn")[: n * F], trace["ffn"][0]),
+        "delta": (plan.read_buffer("delta")[: n * H], trace["delta"][0]),
+        "x": (plan.read_buffer("x_full")[: n * H], trace["x"][0]),
+        "norm": (plan.read_buffer("norm_full")[: n * H], trace["norm"][0]),
+    }
+    errors = {k: _rel(g, r) for k, (g, r) in checks.items()}
+    bad = {k: v for k, v in errors.items() if not (v <= 1e-2)}
+    assert not bad, f"stage errors {errors}"
+    cos = float(np.dot(got, ref) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    assert cos >= 0.9999, f"cosine {cos}"
