@@ -141,8 +141,9 @@ nemo_status nemo_plan_destroy(nemo_plan* plan);
  * parity checks (the reference's buffers of src/webgpu/model.ts:80-94 are
  * debuggable the same way through readF16Buffer, src/main.ts:24-34). Names:
  * "x_full", "norm_full", "x_merged", "norm_merged", "qkv", "q", "k",
- * "attention", "delta", "gate_up", "ffn" (f16, packed rows of the last layer
- * that wrote them) and "embeddings" (float). With out == NULL only *n_bytes is
+ * "attention", "delta" (written only by projections without a K split),
+ * "ffn" (f16, packed rows of the last layer that wrote them) and
+ * "embeddings" (float). With out == NULL only *n_bytes is
  * written (the buffer's capacity). Blocks until the plan's work is done. */
 nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, size_t* n_bytes);
 

@@ -76,7 +76,33 @@ struct DevTensor {
   DevPtr data;   // raw bytes (Q6_K: 208-byte records)
   DevPtr d6;     // Q6_K matrices: per-block f16 scale (null when stored raw)
   size_t bytes = 0;  // GGUF byte size
+  // Gate/up rows reordered per 128-row tile (64 gate rows, then the matching
+  // 64 up rows) for the GEMM's SwiGLU epilogue.
+  bool gate_up_interleaved = false;
 };
+
+// Reorder the rows of a fused gate/up matrix (2F rows: F gate then F up)
+// into 128-row tiles of 64 gate rows followed by the matching 64 up rows.
+void interleave_rows(DevPtr& buf, size_t row_bytes, int64_t F) {
+  DevPtr out = dev_alloc(row_bytes * 2 * F, "interleaved gate/up");
+  const size_t chunk = 64 * row_bytes;
+  const size_t tiles = (size_t)F / 64;
+  hip_check(hipMemcpy2D(out.get(), 2 * chunk, buf.get(), chunk, chunk, tiles, hipMemcpyDeviceToDevice), "interleave");
+  hip_check(hipMemcpy2D((uint8_t*)out.get() + chunk, 2 * chunk, (uint8_t*)buf.get() + F * row_bytes, chunk, chunk,
+                        tiles, hipMemcpyDeviceToDevice),
+            "interleave");
+  buf = std::move(out);
+}
+
+void interleave_gate_up(DevTensor& t, int64_t F) {
+  const int k = (int)t.dims[0];
+  if (t.type == kQ4_K) {
+    interleave_rows(t.data, (size_t)(k / 256) * 144, F);
+  } else {
+    interleave_rows(t.data, (size_t)(k / 256) * 208, F);
+    interleave_rows(t.d6, (size_t)(k / 256) * 2, F);
+  }
+}
 
 size_t ggml_bytes(int type, const std::vector<int64_t>& dims) {
   int64_t n = 1;
@@ -189,7 +215,7 @@ struct nemo_plan {
   int batch = 0, sequence = 0, merged = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
-  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, gate_up, ffn, out, rope;
+  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, ffn, out, rope, partials;
   uint32_t* h_ids = nullptr;   // pinned staging
   float* h_out = nullptr;
   ~nemo_plan() {
@@ -438,7 +464,13 @@ nemo_status nemo_model_finalize(nemo_model* model) {
       fuse_rows(model, p + "ffn_gate_up.weight", {p + "ffn_gate.weight", p + "ffn_up.weight"});
       layers[l].qkv = matrix(model, p + "attn_qkv.weight", H, QKV);
       layers[l].o = matrix(model, p + "attn_output.weight", QW, H);
-      layers[l].gate_up = matrix(model, p + "ffn_gate_up.weight", H, 2 * F);
+      matrix(model, p + "ffn_gate_up.weight", H, 2 * F);  // validates before reordering
+      DevTensor& gu = model->tensors[p + "ffn_gate_up.weight"];
+      if (!gu.gate_up_interleaved) {
+        interleave_gate_up(gu, F);
+        gu.gate_up_interleaved = true;
+      }
+      layers[l].gate_up = as_qweight(gu);
       layers[l].down = matrix(model, p + "ffn_down.weight", F, H);
       layers[l].attn_norm = vec_f32(model, p + "attn_norm.weight", H);
       layers[l].ffn_norm = vec_f32(model, p + "ffn_norm.weight", H);
@@ -484,6 +516,16 @@ nemo_status nemo_model_get_tensor(nemo_model* model, const char* name, int32_t* 
       }
     } else {
       hip_check(hipMemcpy(out, t.data.get(), t.bytes, hipMemcpyDeviceToHost), "download");
+    }
+    if (t.gate_up_interleaved) {  // back to GGUF row order: gate rows, then up rows
+      const int64_t rows = t.dims[1], F = rows / 2;
+      const size_t rb = t.bytes / (size_t)rows;
+      std::vector<uint8_t> tmp((uint8_t*)out, (uint8_t*)out + t.bytes);
+      for (int64_t r = 0; r < rows; ++r) {
+        const int64_t tile = r / 128, local = r % 128;
+        const int64_t orig = local < 64 ? 64 * tile + local : F + 64 * tile + (local - 64);
+        memcpy((uint8_t*)out + orig * rb, tmp.data() + r * rb, rb);
+      }
     }
     *n_bytes = t.bytes;
   });
@@ -548,8 +590,16 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->k = dev_alloc(tf * KW * 2, "key rope");
     p->attn = dev_alloc(tf * QW * 2, "attention");
     p->delta = dev_alloc(tf * H * 2, "residual delta");
-    p->gate_up = dev_alloc(tf * 2 * F * 2, "FFN gate + up");
     p->ffn = dev_alloc(tf * F * 2, "SwiGLU output");
+    // fp32 split-K partial sums of the projections that split K.
+    size_t partial_floats = 0;
+    for (const LayerWeights& w : model->layers) {
+      for (const QWeight* q : {&w.qkv, &w.o, &w.down}) {
+        const int s = gemm_splits(*q);
+        if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
+      }
+    }
+    if (partial_floats) p->partials = dev_alloc(partial_floats * 4, "split-K partial sums");
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
     const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
     p->rope = dev_alloc(table.size() * 4, "RoPE sin/cos table");
@@ -592,7 +642,6 @@ nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, 
     else if (n == "k") src = plan->k.get(), bytes = tf * KW * 2;
     else if (n == "attention") src = plan->attn.get(), bytes = tf * QW * 2;
     else if (n == "delta") src = plan->delta.get(), bytes = tf * H * 2;
-    else if (n == "gate_up") src = plan->gate_up.get(), bytes = tf * 2 * F * 2;
     else if (n == "ffn") src = plan->ffn.get(), bytes = tf * F * 2;
     else if (n == "embeddings") src = plan->out.get(), bytes = (size_t)plan->batch * H * 4;
     else fail(NEMO_ERR_INVALID, "unknown plan buffer " + n);
@@ -649,8 +698,8 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
   uint16_t* k = (uint16_t*)p->k.get();
   uint16_t* attn = (uint16_t*)p->attn.get();
   uint16_t* delta = (uint16_t*)p->delta.get();
-  uint16_t* gu = (uint16_t*)p->gate_up.get();
   uint16_t* ffn = (uint16_t*)p->ffn.get();
+  float* partials = (float*)p->partials.get();
   const float* rope = (const float*)p->rope.get();
 
   mark(0, true);
@@ -672,7 +721,13 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     uint16_t* norm = full ? norm_full : norm_red;
     const LayerWeights& w = m->layers[l];
     mark(2, true);
-    hip_check(launch_gemm(norm, H, w.qkv, qkv, QKV, M, s), "qkv matmul");
+    const int qkv_splits = gemm_splits(w.qkv);
+    if (qkv_splits == 1) {
+      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiStore, 1, qkv, QKV, s), "qkv matmul");
+    } else {
+      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiPartial, qkv_splits, partials, QKV, s), "qkv matmul");
+      hip_check(launch_reduce_partials(partials, qkv_splits, M, QKV, qkv, QKV, s), "qkv reduce");
+    }
     mark(2, false);
     mark(3, true);
     hip_check(launch_rope(qkv, QKV, rows, rope, d.q_heads, d.kv_heads, d.head_dim, q, k, s), "rope");
@@ -680,25 +735,29 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
                                d.kv_heads, d.head_dim, d.kv_stride_threshold, d.kv_stride, attn, s),
               "attention");
     mark(3, false);
-    mark(4, true);
-    hip_check(launch_gemm(attn, QW, w.o, delta, H, M, s), "attention output matmul");
-    mark(4, false);
-    mark(5, true);
-    hip_check(launch_rmsnorm(x, delta, w.ffn_norm, norm, M, H, d.rms_epsilon, s), "rmsnorm");
-    mark(5, false);
-    mark(6, true);
-    hip_check(launch_gemm(norm, H, w.gate_up, gu, 2 * F, M, s), "gate/up matmul");
+    // Residual projection (O or down) then x += delta; RMSNorm. With a K
+    // split, the norm kernel sums the fp32 partials itself.
+    auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
+      const int splits = gemm_splits(wt);
+      mark(stage, true);
+      if (splits == 1)
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s), "residual matmul");
+      else
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s), "residual matmul");
+      mark(stage, false);
+      mark(stage + 1, true);
+      if (splits == 1)
+        hip_check(launch_rmsnorm(x, delta, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
+      else
+        hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
+      mark(stage + 1, false);
+    };
+    residual(attn, QW, w.o, w.ffn_norm, 4);
+    mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
+    hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s), "gate/up matmul");
     mark(6, false);
-    mark(7, true);
-    hip_check(launch_swiglu(gu, M, F, ffn, s), "swiglu");
-    mark(7, false);
-    mark(8, true);
-    hip_check(launch_gemm(ffn, F, w.down, delta, H, M, s), "down matmul");
-    mark(8, false);
-    mark(9, true);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
-    hip_check(launch_rmsnorm(x, delta, next, norm, M, H, d.rms_epsilon, s), "rmsnorm");
-    mark(9, false);
+    residual(ffn, F, w.down, next, 8);
   }
   if (d.merge_after_layer == d.layers) {  // merge after the last layer (models shorter than the reference)
     mark(1, true);

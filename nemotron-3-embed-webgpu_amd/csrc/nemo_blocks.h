@@ -1,0 +1,154 @@
+// Device-side GGML block decoding shared by the GEMM, GEMV and dequant
+// kernels (gfx950).
+//
+// Decoding follows src/gguf/quantization.ts:11-74 (and the WGSL decoders of
+// src/webgpu/quant-matmul.ts:37-154). Every decoded weight is formed in fp32
+// exactly as the reference's JavaScript forms it: d*sc and dmin*m are exact
+// products of an 11-bit and a 6-bit significand, d*sc*q is exact (<= 21
+// bits), so one fmaf(d*sc, q, -dmin*m) rounds the exact value once - the
+// same single rounding as the JS double expression stored to Float32Array.
+// Q6_K: d*scale*(q-32) has <= 23 significant bits and is exact in fp32.
+// MFMA operands are f16(RNE(that fp32 value)), as the WGSL tiles are.
+#pragma once
+
+#include "nemo_common.h"
+#include "nemo_quant.h"
+
+namespace nemo {
+
+typedef float float8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t byte_of(const u32x4& v, int i) {
+  const uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;
+  return (w >> (8 * (i & 3))) & 0xffu;
+}
+
+// Scale and min of sub-block j (0..7) from the 12 packed bytes that follow
+// d and dmin (src/gguf/quantization.ts:11-17). `hdr` is the block's first 16
+// bytes, so scale byte i is byte 4 + i of hdr.
+__device__ __forceinline__ void q4k_scale_min(const u32x4& hdr, int j, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = byte_of(hdr, 4 + j) & 63u;
+    m = byte_of(hdr, 8 + j) & 63u;
+  } else {
+    sc = (byte_of(hdr, 8 + j) & 15u) | ((byte_of(hdr, j) >> 6) << 4);
+    m = (byte_of(hdr, 8 + j) >> 4) | ((byte_of(hdr, 4 + j) >> 6) << 4);
+  }
+}
+
+// fp32 factors of group g (sub-blocks 2g, 2g+1): w = fmaf(dsc, q, ndm).
+__device__ __forceinline__ void q4k_group_factors(const u32x4& hdr, int g, float& dsc0, float& ndm0, float& dsc1,
+                                                  float& ndm1) {
+  const float d = h2f((uint16_t)(hdr.x & 0xffffu));
+  const float dmin = h2f((uint16_t)(hdr.x >> 16));
+  uint32_t sc, m;
+  q4k_scale_min(hdr, 2 * g, sc, m);
+  dsc0 = d * (float)sc;
+  ndm0 = -(dmin * (float)m);
+  q4k_scale_min(hdr, 2 * g + 1, sc, m);
+  dsc1 = d * (float)sc;
+  ndm1 = -(dmin * (float)m);
+}
+
+// Four packed bytes (one value per byte) -> four fp32 values scale*b + bias.
+__device__ __forceinline__ void bytes4_fma(uint32_t w, float scale, float bias, float* out) {
+  out[0] = fmaf(scale, (float)(w & 0xffu), bias);
+  out[1] = fmaf(scale, (float)((w >> 8) & 0xffu), bias);
+  out[2] = fmaf(scale, (float)((w >> 16) & 0xffu), bias);
+  out[3] = fmaf(scale, (float)(w >> 24), bias);
+}
+
+// Round-to-nearest-even f32 -> f16 of eight values (v_cvt_pk_f16_f32 pairs).
+__device__ __forceinline__ half8v to_half8(const float* v) {
+  const float8v f = {v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+  return __builtin_convertvector(f, half8v);
+}
+
+// ---------------------------------------------------------------------------
+// Tile loaders. A loader fetches, for one weight row and one 64-column chunk
+// starting at k0, the bytes of "part" p (0/1) and later expands them to 32
+// f16 values: lo[16] for columns k0+16p..k0+16p+15 and hi[16] for columns
+// k0+32+16p..k0+32+16p+15.
+// ---------------------------------------------------------------------------
+
+struct Q4KFetch {
+  u32x4 hdr;
+  u32x4 q;
+  int g;
+};
+
+__device__ __forceinline__ Q4KFetch q4k_fetch(const QWeight& w, size_t row_bytes, int row, int k0, int p) {
+  const uint8_t* blk = w.blocks + (size_t)row * row_bytes + (size_t)(k0 >> 8) * 144;
+  Q4KFetch f;
+  f.g = (k0 >> 6) & 3;
+  f.hdr = *(const u32x4*)blk;
+  f.q = *(const u32x4*)(blk + 16 + 32 * f.g + 16 * p);
+  return f;
+}
+
+__device__ __forceinline__ void q4k_expand(const Q4KFetch& f, half8v* lo, half8v* hi) {
+  float dsc0, ndm0, dsc1, ndm1;
+  q4k_group_factors(f.hdr, f.g, dsc0, ndm0, dsc1, ndm1);
+  const uint32_t words[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+  float vl[16], vh[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bytes4_fma(words[i] & 0x0f0f0f0fu, dsc0, ndm0, vl + 4 * i);
+    bytes4_fma((words[i] >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh + 4 * i);
+  }
+  lo[0] = to_half8(vl);
+  lo[1] = to_half8(vl + 8);
+  hi[0] = to_half8(vh);
+  hi[1] = to_half8(vh + 8);
+}
+
+struct Q6KFetch {
+  u32x4 qla, qlb, qh;
+  uint32_t scw;
+  uint16_t d;
+  int qp, p;
+};
+
+// Q6_K split layout: record = ql[128] qh[64] scales[16], d separate. Chunk
+// c = (k0 / 64) % 4 covers half c/2, quadrants 2(c%2) and 2(c%2)+1
+// (src/gguf/quantization.ts:53-71).
+__device__ __forceinline__ Q6KFetch q6k_fetch(const QWeight& w, size_t row_bytes, int row, int k0, int p) {
+  const int blk = k0 >> 8;
+  const uint8_t* rec = w.blocks + (size_t)row * row_bytes + (size_t)blk * 208;
+  const int c = (k0 >> 6) & 3, half = c >> 1;
+  Q6KFetch f;
+  f.qp = c & 1;
+  f.p = p;
+  f.qla = *(const u32x4*)(rec + 64 * half + 16 * p);
+  f.qlb = *(const u32x4*)(rec + 64 * half + 32 + 16 * p);
+  f.qh = *(const u32x4*)(rec + 128 + 32 * half + 16 * p);
+  f.scw = *(const uint32_t*)(rec + 192 + 8 * half + 4 * f.qp);
+  f.d = w.d[(size_t)row * (w.k >> 8) + blk];
+  return f;
+}
+
+__device__ __forceinline__ void q6k_expand(const Q6KFetch& f, half8v* lo, half8v* hi) {
+  const float d = h2f(f.d);
+  // scale of quadrant 2qp for lanes 16p..16p+15 is scales[8h + p + 4qp]
+  // (byte p of scw); quadrant 2qp+1 uses scales[8h + p + 4qp + 2].
+  const float dsc0 = d * (float)(int8_t)((f.scw >> (8 * f.p)) & 0xffu);
+  const float dsc1 = d * (float)(int8_t)((f.scw >> (8 * (f.p + 2))) & 0xffu);
+  const int s0 = 4 * f.qp, s1 = 4 * f.qp + 2;
+  const uint32_t la[4] = {f.qla.x, f.qla.y, f.qla.z, f.qla.w};
+  const uint32_t lb[4] = {f.qlb.x, f.qlb.y, f.qlb.z, f.qlb.w};
+  const uint32_t hh[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
+  float vl[16], vh[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t q0 = ((la[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s0) & 0x03030303u) << 4);
+    const uint32_t q1 = ((lb[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s1) & 0x03030303u) << 4);
+    bytes4_fma(q0, dsc0, -32.0f * dsc0, vl + 4 * i);
+    bytes4_fma(q1, dsc1, -32.0f * dsc1, vh + 4 * i);
+  }
+  lo[0] = to_half8(vl);
+  lo[1] = to_half8(vl + 8);
+  hi[0] = to_half8(vh);
+  hi[1] = to_half8(vh + 8);
+}
+
+}  // namespace nemo

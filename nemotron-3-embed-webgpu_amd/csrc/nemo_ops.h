@@ -19,6 +19,10 @@ hipError_t launch_embed(const uint32_t* ids, int padded_seq, const Ragged& rows,
 hipError_t launch_rmsnorm(uint16_t* x, const uint16_t* delta, const float* w, uint16_t* normalized, int rows,
                           int hidden, float eps, hipStream_t stream);
 
+// The same with delta = f16(sum over s of partials[s][row][:]) (split order).
+hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int splits, const float* w,
+                                   uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream);
+
 // Rotate adjacent pairs of the query and key heads of qkv into q [t, Hq, hd]
 // and k [t, Hkv, hd]; position = row index within its request.
 hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, const float* table, int q_heads,

@@ -4,6 +4,7 @@
 //
 // Semantics follow src/webgpu/ops.ts (cited per kernel). Storage is f16 as in
 // the reference's buffers; arithmetic is fp32.
+#include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_ops.h"
 #include "nemo_quant.h"
@@ -87,23 +88,42 @@ hipError_t launch_embed(const uint32_t* ids, int padded_seq, const Ragged& rows,
 
 // ---------------------------------------------------------------------------
 // Residual add + RMSNorm (src/webgpu/ops.ts:21-56). One workgroup per row,
-// 8 values (16 bytes) per thread and pass.
+// 8 values (16 bytes) per thread and pass. The residual delta is either an
+// f16 row or the fp32 split-K partial sums of the producing GEMM, summed in
+// split order and rounded to f16 (the reference's delta buffer is f16).
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
-                                                      const float* __restrict__ w, uint16_t* __restrict__ out,
-                                                      int hidden, float eps) {
+template <bool PARTIALS>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, const void* __restrict__ delta,
+                                                      int splits, int rows, const float* __restrict__ w,
+                                                      uint16_t* __restrict__ out, int hidden, float eps) {
   __shared__ float scratch[16];
   const size_t base = (size_t)blockIdx.x * hidden;
   float sum = 0.f;
   for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
     half8v xv = *(const half8v*)(x + base + c);
     if (delta) {
-      const half8v dv = *(const half8v*)(delta + base + c);
+      float dv[8];
+      if constexpr (PARTIALS) {
+        const float* p = (const float*)delta + base + c;
+        float4v a = *(const float4v*)p, b = *(const float4v*)(p + 4);
+        for (int s = 1; s < splits; ++s) {
+          const float* q = p + (size_t)s * rows * hidden;
+          a += *(const float4v*)q;
+          b += *(const float4v*)(q + 4);
+        }
+        const float raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dv[i] = (float)(half_t)raw[i];
+      } else {
+        const half8v d16 = *(const half8v*)((const uint16_t*)delta + base + c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dv[i] = (float)d16[i];
+      }
       half8v stored;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float v = (float)xv[i] + (float)dv[i];
+        const float v = (float)xv[i] + dv[i];
         sum += v * v;  // the unrounded sum, as ops.ts:39-40
         stored[i] = (half_t)v;
       }
@@ -129,7 +149,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, 
 hipError_t launch_rmsnorm(uint16_t* x, const uint16_t* delta, const float* w, uint16_t* normalized, int rows,
                           int hidden, float eps, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
-  rmsnorm_kernel<<<rows, 256, 0, stream>>>(x, delta, w, normalized, hidden, eps);
+  rmsnorm_kernel<false><<<rows, 256, 0, stream>>>(x, delta, 1, rows, w, normalized, hidden, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int splits, const float* w,
+                                   uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  rmsnorm_kernel<true><<<rows, 256, 0, stream>>>(x, partials, splits, rows, w, normalized, hidden, eps);
   return hipGetLastError();
 }
 
@@ -169,26 +196,36 @@ hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, 
 }
 
 // ---------------------------------------------------------------------------
-// Bidirectional GQA attention (src/webgpu/ops.ts:213-293, 295-362).
-// For request b with n valid rows, query i attends keys 0, s, 2s, ... < n
-// (s = key_stride if n > stride_threshold, else 1) with scores
-// q.k * head_dim^-1/2 * temperature(i), temperature = 1 + 0.1 ln(floor(i /
-// 16384) + 1) for i >= 16384 (ops.ts:241). Online softmax in fp32.
-// Workgroup = 64 queries of one request and head; 4 lanes per query, each
-// holding a quarter of the head dimension. Keys/values staged in LDS tiles.
+// Bidirectional GQA flash attention on MFMA (src/webgpu/ops.ts:213-293,
+// 295-362). For request b with n valid rows, query i attends keys
+// 0, s, 2s, ... < n (s = key_stride if n > stride_threshold, else 1) with
+// scores q.k * head_dim^-1/2 * temperature(i), temperature = 1 + 0.1
+// ln(floor(i / 16384) + 1) for i >= 16384 (ops.ts:241); online softmax in
+// fp32, output f16.
+//
+// Workgroup = one request, one KV head, 32 queries; wave w handles query
+// head kv_head * group + w, so the staged K/V tiles serve the whole GQA
+// group. Scores are computed transposed, S^T = K Q^T (32 keys x 32 queries
+// per v_mfma_f32_32x32x16_f16), so lane l always holds query l%32: the
+// softmax max/sum are per-lane scalars (one cross-half exchange), and the
+// rescale of the output accumulators is a per-lane multiply. The output is
+// accumulated transposed too, O^T = V^T P^T, with V staged transposed in LDS
+// and P fed from the score registers: the MFMA's k index is mapped to the
+// keys a lane holds (the key order of a sum is free; A and B agree on it).
 // ---------------------------------------------------------------------------
 
-constexpr int kAttnQ = 64, kAttnKeys = 64;
+constexpr int kAttnQ = 32, kAttnKeys = 32, kVtPad = 40;
 
 template <int HD>
-__global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+__global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                         const uint16_t* __restrict__ v_base, int v_stride,
                                                         Ragged rows, int q_heads, int kv_heads, int stride_threshold,
                                                         int key_stride_long, uint16_t* __restrict__ out) {
-  constexpr int QD = HD / 4;
-  __shared__ __attribute__((aligned(16))) half_t sK[kAttnKeys * HD];
-  __shared__ __attribute__((aligned(16))) half_t sV[kAttnKeys * HD];
-  // Locate (request, query tile) of this workgroup.
+  constexpr int KP = HD + 8;  // padded K row (halves)
+  constexpr int DC = HD / 16; // 16-wide d chunks of the score MFMAs
+  constexpr int DB = HD / 32; // 32-wide d blocks of the output
+  __shared__ __attribute__((aligned(16))) half_t sK[kAttnKeys * KP];
+  __shared__ __attribute__((aligned(16))) half_t sVt[HD * kVtPad];
   int b = 0, tile = blockIdx.x;
   for (; b < rows.count; ++b) {
     const int n = rows.start[b + 1] - rows.start[b];
@@ -199,83 +236,105 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restri
   if (b >= rows.count) return;
   const int row0 = rows.start[b];
   const int n = rows.start[b + 1] - row0;
-  const int h = blockIdx.y;
-  const int kvh = h / (q_heads / kv_heads);
-  const int qi = tile * kAttnQ + (threadIdx.x >> 2);
-  const int part = threadIdx.x & 3;
+  const int kvh = blockIdx.y;
+  const int group = q_heads / kv_heads;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hl = lane >> 5;
+  const int h = kvh * group + wave;
+  const int qi = tile * kAttnQ + (lane & 31);
   const int key_stride = n > stride_threshold ? key_stride_long : 1;
-  const float temperature = qi >= 16384 ? logf(floorf((float)qi / 16384.0f) + 1.0f) * 0.1f + 1.0f : 1.0f;
-  const float scale = (1.0f / sqrtf((float)HD)) * temperature;
-
-  float qv[QD], acc[QD];
-  {
-    const int qrow = min(qi, n - 1);
-    const uint16_t* qp = q + ((size_t)(row0 + qrow) * q_heads + h) * HD + part * QD;
-#pragma unroll
-    for (int i = 0; i < QD; i += 8) {
-      const half8v hv = *(const half8v*)(qp + i);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qv[i + e] = (float)hv[e];
-        acc[i + e] = 0.f;
-      }
-    }
-  }
-  float mx = -INFINITY, den = 0.f;
   const int n_keys = (n + key_stride - 1) / key_stride;
+  const float temperature = qi >= 16384 ? logf(floorf((float)qi / 16384.0f) + 1.0f) * 0.1f + 1.0f : 1.0f;
+  const float scale2 = (1.0f / sqrtf((float)HD)) * temperature * 1.4426950408889634f;
+
+  half8v qf[DC];
+  {
+    const uint16_t* qp = q + ((size_t)(row0 + min(qi, n - 1)) * q_heads + h) * HD + 8 * hl;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qf[c] = *(const half8v*)(qp + 16 * c);
+  }
+  float16v o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
   for (int kb = 0; kb < n_keys; kb += kAttnKeys) {
     __syncthreads();
-    // Stage up to 64 sampled keys and values: 8 halves per thread and pass.
     for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
       const int j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-      const int kj = kb + j;
-      u32x4 kv4 = {0u, 0u, 0u, 0u}, vv4 = {0u, 0u, 0u, 0u};
-      if (kj < n_keys) {
-        const int trow = row0 + kj * key_stride;
+      u32x4 kv4 = {0u, 0u, 0u, 0u};
+      half8v vv = {};
+      if (kb + j < n_keys) {
+        const int trow = row0 + (kb + j) * key_stride;
         kv4 = *(const u32x4*)(k + ((size_t)trow * kv_heads + kvh) * HD + c);
-        vv4 = *(const u32x4*)(v_base + (size_t)trow * v_stride + kvh * HD + c);
+        vv = *(const half8v*)(v_base + (size_t)trow * v_stride + kvh * HD + c);
       }
-      *(u32x4*)&sK[j * HD + c] = kv4;
-      *(u32x4*)&sV[j * HD + c] = vv4;
+      *(u32x4*)&sK[j * KP + c] = kv4;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sVt[(c + e) * kVtPad + j] = vv[e];
     }
     __syncthreads();
-    const int jn = min(kAttnKeys, n_keys - kb);
-    for (int j = 0; j < jn; ++j) {
-      const half_t* kr = &sK[j * HD + part * QD];
-      float s = 0.f;
+    // S^T block: lane holds query l%32, key kb + 8(r/4) + 4hl + r%4.
+    float16v s;
 #pragma unroll
-      for (int i = 0; i < QD; i += 8) {
-        const half8v kh = *(const half8v*)(kr + i);
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = fmaf(qv[i + e], (float)kh[e], s);
-      }
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s *= scale;
-      const float mnew = fmaxf(mx, s);
-      const float alpha = expf(mx - mnew);
-      const float p = expf(s - mnew);
-      den = den * alpha + p;
-      mx = mnew;
-      const half_t* vr = &sV[j * HD + part * QD];
+    for (int c = 0; c < DC; ++c) {
+      const half8v a = *(const half8v*)&sK[(lane & 31) * KP + 16 * c + 8 * hl];
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
+    }
+    float bm = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < QD; i += 8) {
-        const half8v vh = *(const half8v*)(vr + i);
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
+      s[r] = key < n_keys ? s[r] * scale2 : -INFINITY;
+      bm = fmaxf(bm, s[r]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float alpha = exp2f(m - mn);
+    float ps = 0.f;
+    float p[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i + e] = fmaf(p, (float)vh[e], acc[i + e] * alpha);
+    for (int r = 0; r < 16; ++r) {
+      p[r] = exp2f(s[r] - mn);
+      ps += p[r];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    // O^T += V^T P^T over two 16-key chunks: MFMA k slot 8hl + e of chunk c2
+    // is key 16c2 + 8(e/4) + 4hl + e%4 = score register 8c2 + e.
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      const half8v pb = to_half8(p + 8 * c2);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half_t* vr = &sVt[(32 * db + (lane & 31)) * kVtPad + 16 * c2 + 4 * hl];
+        const half4v v0 = *(const half4v*)vr;
+        const half4v v1 = *(const half4v*)(vr + 8);
+        const half8v a = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[db], 0, 0, 0);
       }
     }
   }
   if (qi >= n) return;
-  const float inv = 1.0f / den;
-  uint16_t* op = out + ((size_t)(row0 + qi) * q_heads + h) * HD + part * QD;
+  const float inv = 1.0f / lsum;
+  uint16_t* op = out + ((size_t)(row0 + qi) * q_heads + h) * HD;
 #pragma unroll
-  for (int i = 0; i < QD; i += 8) {
-    half8v o;
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (half_t)(acc[i + e] * inv);
-    *(half8v*)(op + i) = o;
-  }
+    for (int j = 0; j < 4; ++j) {
+      // registers 4j..4j+3 hold d = 32db + 8j + 4hl + 0..3 (contiguous)
+      const half4v hv = {(half_t)(o[db][4 * j] * inv), (half_t)(o[db][4 * j + 1] * inv),
+                         (half_t)(o[db][4 * j + 2] * inv), (half_t)(o[db][4 * j + 3] * inv)};
+      *(half4v*)(op + 32 * db + 8 * j + 4 * hl) = hv;
+    }
 }
 
 hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v_base, int v_stride,
@@ -284,13 +343,15 @@ hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t
   int tiles = 0;
   for (int b = 0; b < rows.count; ++b) tiles += (rows.start[b + 1] - rows.start[b] + kAttnQ - 1) / kAttnQ;
   if (tiles == 0) return hipSuccess;
-  dim3 grid(tiles, q_heads);
+  const int group = q_heads / kv_heads;
+  if (group < 1 || group > 8 || q_heads % kv_heads) return hipErrorInvalidValue;
+  dim3 grid(tiles, kv_heads);
   if (head_dim == 64)
-    attention_kernel<64><<<grid, 256, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads, stride_threshold,
-                                                   key_stride, out);
+    attention_kernel<64><<<grid, 64 * group, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads,
+                                                          stride_threshold, key_stride, out);
   else if (head_dim == 128)
-    attention_kernel<128><<<grid, 256, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads, stride_threshold,
-                                                    key_stride, out);
+    attention_kernel<128><<<grid, 64 * group, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads,
+                                                           stride_threshold, key_stride, out);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -370,7 +431,7 @@ hipError_t launch_merge(const uint16_t* in, const Ragged& src, const Ragged& dst
 
 // ---------------------------------------------------------------------------
 // Mean pool + L2 normalise (src/webgpu/ops.ts:596-615). One workgroup per
-// request.
+// request; each thread owns 8 consecutive columns (16-byte loads per row).
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void mean_pool_kernel(const uint16_t* __restrict__ norm, Ragged rows, int hidden,
@@ -379,15 +440,24 @@ __global__ __launch_bounds__(256) void mean_pool_kernel(const uint16_t* __restri
   const int b = blockIdx.x;
   const int r0 = rows.start[b], n = rows.start[b + 1] - r0;
   float sq = 0.f;
-  for (int d = threadIdx.x; d < hidden; d += blockDim.x) {
-    float total = 0.f;
-    for (int p = 0; p < n; ++p) total += h2f(norm[(size_t)(r0 + p) * hidden + d]);
-    const float mean = total / (float)n;
-    out[(size_t)b * hidden + d] = mean;
-    sq += mean * mean;
+  for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
+    float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < n; ++p) {
+      const half8v v = *(const half8v*)(norm + (size_t)(r0 + p) * hidden + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) total[e] += (float)v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float mean = total[e] / (float)n;
+      out[(size_t)b * hidden + c + e] = mean;
+      sq += mean * mean;
+    }
   }
   const float inv = 1.0f / sqrtf(block_sum(sq, scratch));
-  for (int d = threadIdx.x; d < hidden; d += blockDim.x) out[(size_t)b * hidden + d] *= inv;
+  for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[(size_t)b * hidden + c + e] *= inv;
 }
 
 hipError_t launch_mean_pool(const uint16_t* norm, const Ragged& rows, int hidden, float* out, hipStream_t stream) {

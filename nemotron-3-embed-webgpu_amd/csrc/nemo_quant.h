@@ -30,10 +30,29 @@ __host__ __device__ inline size_t qweight_row_bytes(int type, int k) {
   return type == kQ4_K ? (size_t)(k / 256) * 144 : (size_t)(k / 256) * 208;
 }
 
+// GEMM epilogues.
+enum GemmEpilogue : int {
+  kEpiStore = 0,    // out f16 [m, ldo]: f16(sum)
+  kEpiPartial = 1,  // out float [splits][m][ldo]: the fp32 sum of each K split
+  kEpiSwiGLU = 2,   // out f16 [m, ldo]: silu(g) * u over rows interleaved per 128-row tile
+};
+
 // Y[m, n] = f16( sum_k X[m, k] * W[n, k] ), fp32 accumulate. X is f16 with
-// row stride ldx, Y f16 with row stride ldy. Chooses the MFMA GEMM.
+// row stride ldx, Y f16 with row stride ldy (MFMA GEMM, no K split).
 hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
                        hipStream_t stream);
+
+// The K-split count the encoder uses for `w`: a function of the weight's
+// shape only.
+int gemm_splits(const QWeight& w);
+
+// The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial.
+hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
+                          int ldo, hipStream_t stream);
+
+// y[m, n] = f16(sum over s of partials[s][m][n]) in split order.
+hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
+                                  hipStream_t stream);
 
 // Small-M path (m <= 16): split-K wavefront GEMV with a deterministic
 // reduction through `partials` (float, at least gemv_partials_floats()).

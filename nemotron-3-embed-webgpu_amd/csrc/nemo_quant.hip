@@ -1,270 +1,19 @@
-// Quantized-weight kernels for gfx950: GGML Q4_K / Q6_K / Q4_0 block
-// decoding, the fused dequant + MFMA GEMM (batched tokens) and the split-K
-// wavefront GEMV (m <= 16).
-//
-// Decoding follows src/gguf/quantization.ts:11-74 (and the WGSL decoders of
-// src/webgpu/quant-matmul.ts:37-154). Every decoded weight is formed in fp32
-// exactly as the reference's JavaScript forms it: d*sc and dmin*m are exact
-// products of an 11-bit and a 6-bit significand, d*sc*q is exact (<= 21
-// bits), so one fmaf(d*sc, q, -dmin*m) rounds the exact value once - the
-// same single rounding as the JS double expression stored to Float32Array.
-// Q6_K: d*scale*(q-32) has <= 23 significant bits and is exact in fp32.
-// The GEMM feeds MFMA with f16(RNE(that fp32 value)), as the WGSL tiles do.
+// Quantized-weight kernels for gfx950 besides the GEMM: the split-K
+// wavefront GEMV (m <= 16), GGML Q4_K / Q6_K / Q4_0 block decoding to
+// float32/f16 (bit-exact with src/gguf/quantization.ts:19-74), and the
+// fixed-order reduction of split-K partial sums.
+#include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_quant.h"
 
 namespace nemo {
 
 // ---------------------------------------------------------------------------
-// Block field helpers
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ uint32_t byte_of(const u32x4& v, int i) {
-  const uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;
-  return (w >> (8 * (i & 3))) & 0xffu;
-}
-
-// Scale and min of sub-block j (0..7) from the 12 packed bytes that follow
-// d and dmin (src/gguf/quantization.ts:11-17). `hdr` is the block's first 16
-// bytes, so scale byte i is byte 4 + i of hdr.
-__device__ __forceinline__ void q4k_scale_min(const u32x4& hdr, int j, uint32_t& sc, uint32_t& m) {
-  if (j < 4) {
-    sc = byte_of(hdr, 4 + j) & 63u;
-    m = byte_of(hdr, 8 + j) & 63u;
-  } else {
-    sc = (byte_of(hdr, 8 + j) & 15u) | ((byte_of(hdr, j) >> 6) << 4);
-    m = (byte_of(hdr, 8 + j) >> 4) | ((byte_of(hdr, 4 + j) >> 6) << 4);
-  }
-}
-
-// fp32 factors of group g (sub-blocks 2g, 2g+1): w = fmaf(dsc, q, ndm).
-__device__ __forceinline__ void q4k_group_factors(const u32x4& hdr, int g, float& dsc0, float& ndm0,
-                                                  float& dsc1, float& ndm1) {
-  const float d = h2f((uint16_t)(hdr.x & 0xffffu));
-  const float dmin = h2f((uint16_t)(hdr.x >> 16));
-  uint32_t sc, m;
-  q4k_scale_min(hdr, 2 * g, sc, m);
-  dsc0 = d * (float)sc;
-  ndm0 = -(dmin * (float)m);
-  q4k_scale_min(hdr, 2 * g + 1, sc, m);
-  dsc1 = d * (float)sc;
-  ndm1 = -(dmin * (float)m);
-}
-
-// Four packed bytes (one value per byte) -> four fp32 values scale*b + bias.
-__device__ __forceinline__ void bytes4_fma(uint32_t w, float scale, float bias, float* out) {
-  out[0] = fmaf(scale, (float)(w & 0xffu), bias);
-  out[1] = fmaf(scale, (float)((w >> 8) & 0xffu), bias);
-  out[2] = fmaf(scale, (float)((w >> 16) & 0xffu), bias);
-  out[3] = fmaf(scale, (float)(w >> 24), bias);
-}
-
-__device__ __forceinline__ half8v to_half8(const float* v) {
-  half8v h;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = (half_t)v[i];
-  return h;
-}
-
-// ---------------------------------------------------------------------------
-// W tile loaders. A loader fetches, for one weight row and one 64-column
-// chunk starting at k0, the bytes of "part" p (0/1) and later expands them to
-// 32 f16 values: lo[16] for columns k0+16p..k0+16p+15 and hi[16] for columns
-// k0+32+16p..k0+32+16p+15.
-// ---------------------------------------------------------------------------
-
-struct Q4KFetch {
-  u32x4 hdr;
-  u32x4 q;
-  int g;
-};
-
-__device__ __forceinline__ Q4KFetch q4k_fetch(const QWeight& w, size_t row_bytes, int row, int k0, int p) {
-  const uint8_t* blk = w.blocks + (size_t)row * row_bytes + (size_t)(k0 >> 8) * 144;
-  Q4KFetch f;
-  f.g = (k0 >> 6) & 3;
-  f.hdr = *(const u32x4*)blk;
-  f.q = *(const u32x4*)(blk + 16 + 32 * f.g + 16 * p);
-  return f;
-}
-
-__device__ __forceinline__ void q4k_expand(const Q4KFetch& f, half8v* lo, half8v* hi) {
-  float dsc0, ndm0, dsc1, ndm1;
-  q4k_group_factors(f.hdr, f.g, dsc0, ndm0, dsc1, ndm1);
-  const uint32_t words[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
-  float vl[16], vh[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bytes4_fma(words[i] & 0x0f0f0f0fu, dsc0, ndm0, vl + 4 * i);
-    bytes4_fma((words[i] >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh + 4 * i);
-  }
-  lo[0] = to_half8(vl);
-  lo[1] = to_half8(vl + 8);
-  hi[0] = to_half8(vh);
-  hi[1] = to_half8(vh + 8);
-}
-
-struct Q6KFetch {
-  u32x4 qla, qlb, qh;
-  uint32_t scw;
-  uint16_t d;
-  int qp, p;
-};
-
-// Q6_K split layout: record = ql[128] qh[64] scales[16], d separate. Chunk
-// c = (k0 / 64) % 4 covers half c/2, quadrants 2(c%2) and 2(c%2)+1
-// (src/gguf/quantization.ts:53-71).
-__device__ __forceinline__ Q6KFetch q6k_fetch(const QWeight& w, size_t row_bytes, int row, int k0, int p) {
-  const int blk = k0 >> 8;
-  const uint8_t* rec = w.blocks + (size_t)row * row_bytes + (size_t)blk * 208;
-  const int c = (k0 >> 6) & 3, half = c >> 1;
-  Q6KFetch f;
-  f.qp = c & 1;
-  f.p = p;
-  f.qla = *(const u32x4*)(rec + 64 * half + 16 * p);
-  f.qlb = *(const u32x4*)(rec + 64 * half + 32 + 16 * p);
-  f.qh = *(const u32x4*)(rec + 128 + 32 * half + 16 * p);
-  f.scw = *(const uint32_t*)(rec + 192 + 8 * half + 4 * f.qp);
-  f.d = w.d[(size_t)row * (w.k >> 8) + blk];
-  return f;
-}
-
-__device__ __forceinline__ void q6k_expand(const Q6KFetch& f, half8v* lo, half8v* hi) {
-  const float d = h2f(f.d);
-  // scale of quadrant 2qp for lanes 16p..16p+15 is scales[8h + p + 4qp]
-  // (byte p of scw); quadrant 2qp+1 uses scales[8h + p + 4qp + 2].
-  const float dsc0 = d * (float)(int8_t)((f.scw >> (8 * f.p)) & 0xffu);
-  const float dsc1 = d * (float)(int8_t)((f.scw >> (8 * (f.p + 2))) & 0xffu);
-  const int s0 = 4 * f.qp, s1 = 4 * f.qp + 2;
-  const uint32_t la[4] = {f.qla.x, f.qla.y, f.qla.z, f.qla.w};
-  const uint32_t lb[4] = {f.qlb.x, f.qlb.y, f.qlb.z, f.qlb.w};
-  const uint32_t hh[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
-  float vl[16], vh[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t q0 = ((la[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s0) & 0x03030303u) << 4);
-    const uint32_t q1 = ((lb[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s1) & 0x03030303u) << 4);
-    bytes4_fma(q0, dsc0, -32.0f * dsc0, vl + 4 * i);
-    bytes4_fma(q1, dsc1, -32.0f * dsc1, vh + 4 * i);
-  }
-  lo[0] = to_half8(vl);
-  lo[1] = to_half8(vl + 8);
-  hi[0] = to_half8(vh);
-  hi[1] = to_half8(vh + 8);
-}
-
-// ---------------------------------------------------------------------------
-// Fused dequant + MFMA GEMM.  Y[M,N] = X[M,K] * W[N,K]^T.
-// Tile 128 x 128 x 64, 256 threads = 4 waves in a 2 x 2 grid, each wave a
-// 64 x 64 block of four v_mfma_f32_32x32x16_f16 accumulators. W is decoded
-// once per workgroup into LDS and shared by all 128 rows of the M tile.
-// Global loads of step k+1 are issued before the MFMAs of step k.
-// ---------------------------------------------------------------------------
-
-constexpr int kBM = 128, kBN = 128, kBK = 64, kLdsK = kBK + 8;  // 144-byte LDS rows
-
-template <int TYPE>
-__global__ __launch_bounds__(256, 2) void gemm_q_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w,
-                                                        uint16_t* __restrict__ y, int ldy, int M) {
-  __shared__ __attribute__((aligned(16))) half_t sA[kBM * kLdsK];
-  __shared__ __attribute__((aligned(16))) half_t sB[kBN * kLdsK];
-  const int N = w.n, K = w.k;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const size_t row_bytes = qweight_row_bytes(TYPE, K);
-
-  // X loader: 4 passes of 32 rows; 8 threads cover one row's 64 columns.
-  const int xr = tid >> 3, xc = (tid & 7) * 8;
-  const uint16_t* xrow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = min(m0 + i * 32 + xr, M - 1);
-    xrow[i] = x + (size_t)r * ldx + xc;
-  }
-  // W loader: 2 threads per weight row.
-  const int wr = tid >> 1, wp = tid & 1;
-  const int wrow = min(n0 + wr, N - 1);
-
-  u32x4 xa[4];
-  Q4KFetch f4;
-  Q6KFetch f6;
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xa[i] = *(const u32x4*)(xrow[i] + k0);
-    if constexpr (TYPE == kQ4_K) f4 = q4k_fetch(w, row_bytes, wrow, k0, wp);
-    else f6 = q6k_fetch(w, row_bytes, wrow, k0, wp);
-  };
-
-  float16v acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  fetch(0);
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    half8v lo[2], hi[2];
-    if constexpr (TYPE == kQ4_K) q4k_expand(f4, lo, hi);
-    else q6k_expand(f6, lo, hi);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4*)&sA[(i * 32 + xr) * kLdsK + xc] = xa[i];
-    half_t* brow = &sB[wr * kLdsK];
-    *(half8v*)(brow + 16 * wp) = lo[0];
-    *(half8v*)(brow + 16 * wp + 8) = lo[1];
-    *(half8v*)(brow + 32 + 16 * wp) = hi[0];
-    *(half8v*)(brow + 32 + 16 * wp + 8) = hi[1];
-    __syncthreads();
-    if (k0 + kBK < K) fetch(k0 + kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int kk = ks * 16 + (lane >> 5) * 8;
-      half8v af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *(const half8v*)&sA[(wm * 64 + i * 32 + (lane & 31)) * kLdsK + kk];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = *(const half8v*)&sB[(wn * 64 + j * 32 + (lane & 31)) * kLdsK + kk];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // D layout of a 32x32 MFMA block: lane l, register r -> row
-  // 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (col >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < M) y[(size_t)row * ldy + col] = f2h(acc[i][j][r]);
-      }
-    }
-}
-
-hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, hipStream_t stream) {
-  if (m <= 0) return hipSuccess;
-  dim3 grid((w.n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-  if (w.type == kQ4_K) gemm_q_kernel<kQ4_K><<<grid, 256, 0, stream>>>(x, ldx, w, y, ldy, m);
-  else if (w.type == kQ6_K) gemm_q_kernel<kQ6_K><<<grid, 256, 0, stream>>>(x, ldx, w, y, ldy, m);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
 // Split-K GEMV for m <= 16 using v_mfma_f32_16x16x32_f16: a wave owns 16
 // weight rows and one K slice; lane l works on row n0 + l%16 and the 8-column
 // slice 8*(l/16) of each 32-column MFMA step. Each lane decodes its own
 // weights straight into the B fragment (no LDS). Partials of the K slices are
-// summed in a fixed order by gemv_reduce_kernel (deterministic).
+// summed in a fixed order by reduce_partials_kernel (deterministic).
 // ---------------------------------------------------------------------------
 
 constexpr int kGemvWaves = 4;
@@ -353,13 +102,21 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_q_kernel(const uint16_t*
   }
 }
 
-__global__ void gemv_reduce_kernel(const float* __restrict__ partials, int splits, int M, int N,
-                                   uint16_t* __restrict__ y, int ldy) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= M * N) return;
+__global__ void reduce_partials_kernel(const float* __restrict__ partials, int splits, int M, int N,
+                                       uint16_t* __restrict__ y, int ldy) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
   float s = 0.f;
   for (int i = 0; i < splits; ++i) s += partials[(size_t)i * M * N + idx];
   y[(size_t)(idx / N) * ldy + (idx % N)] = f2h(s);
+}
+
+hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
+                                  hipStream_t stream) {
+  const int64_t total = (int64_t)m * n;
+  if (total <= 0) return hipSuccess;
+  reduce_partials_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(partials, splits, m, n, y, ldy);
+  return hipGetLastError();
 }
 
 static int gemv_splits(const QWeight& w) {
@@ -390,10 +147,7 @@ hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
     gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, partials, y, ldy);
   else
     return hipErrorInvalidValue;
-  if (splits > 1) {
-    const int total = m * w.n;
-    gemv_reduce_kernel<<<(total + 255) / 256, 256, 0, stream>>>(partials, splits, m, w.n, y, ldy);
-  }
+  if (splits > 1) return launch_reduce_partials(partials, splits, m, w.n, y, ldy, stream);
   return hipGetLastError();
 }
 

@@ -20,9 +20,10 @@ def _rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-@pytest.mark.parametrize("hd,emb", [(64, 1), (128, 1), (64, 14), (128, 14)])
-def test_one_layer_stages(torch_cuda, hd, emb):
-    H, F, V = 256, 512, 300
+@pytest.mark.parametrize("hd,emb,F", [(64, 1, 512), (128, 1, 512), (64, 14, 512), (128, 14, 512),
+                                      (64, 1, 4096)])  # F 4096: the down projection splits K four ways
+def test_one_layer_stages(torch_cuda, hd, emb, F):
+    H, V = 256, 300
     Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
     dims = rt.make_dims(hidden=H, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=F, layers=1, vocab=V,
                         merge_after_layer=1)
@@ -41,9 +42,7 @@ def test_one_layer_stages(torch_cuda, hd, emb):
         "q": (plan.read_buffer("q")[: n * Hq * hd], trace["q"][0]),
         "k": (plan.read_buffer("k")[: n * Hkv * hd], trace["k"][0]),
         "attention": (plan.read_buffer("attention")[: n * Hq * hd], trace["attention"][0]),
-        "gate_up": (plan.read_buffer("gate_up")[: n * 2 * F], trace["gate_up"][0]),
         "ffn": (plan.read_buffer("ffn")[: n * F], trace["ffn"][0]),
-        "delta": (plan.read_buffer("delta")[: n * H], trace["delta"][0]),
         "x": (plan.read_buffer("x_full")[: n * H], trace["x"][0]),
         "norm": (plan.read_buffer("norm_full")[: n * H], trace["norm"][0]),
     }
