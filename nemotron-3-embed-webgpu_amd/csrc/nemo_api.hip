@@ -208,6 +208,7 @@ struct nemo_weight {
   DevTensor t;
   QWeight w{};
   DevPtr partials;
+  DevPtr wexp;  // f16 expansion for the two-pass GEMM, allocated on first use
 };
 
 struct nemo_plan {
@@ -215,7 +216,7 @@ struct nemo_plan {
   int batch = 0, sequence = 0, merged = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
-  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, ffn, out, rope, partials;
+  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, ffn, out, rope, partials, wexp;
   uint32_t* h_ids = nullptr;   // pinned staging
   float* h_out = nullptr;
   ~nemo_plan() {
@@ -600,6 +601,13 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
       }
     }
     if (partial_floats) p->partials = dev_alloc(partial_floats * 4, "split-K partial sums");
+    // f16 expansion of the largest matrix that takes the two-pass GEMM.
+    size_t wexp_halves = 0;
+    for (const LayerWeights& w : model->layers)
+      for (const QWeight* q : {&w.qkv, &w.o, &w.gate_up, &w.down})
+        if (gemm_two_pass(*q, (int)tf, gemm_splits(*q)))
+          wexp_halves = std::max(wexp_halves, (size_t)q->n * q->k);
+    if (wexp_halves) p->wexp = dev_alloc(wexp_halves * 2, "f16 weight expansion");
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
     const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
     p->rope = dev_alloc(table.size() * 4, "RoPE sin/cos table");
@@ -700,6 +708,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
   uint16_t* delta = (uint16_t*)p->delta.get();
   uint16_t* ffn = (uint16_t*)p->ffn.get();
   float* partials = (float*)p->partials.get();
+  uint16_t* wexp = (uint16_t*)p->wexp.get();
   const float* rope = (const float*)p->rope.get();
 
   mark(0, true);
@@ -723,9 +732,9 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     mark(2, true);
     const int qkv_splits = gemm_splits(w.qkv);
     if (qkv_splits == 1) {
-      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiStore, 1, qkv, QKV, s), "qkv matmul");
+      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiStore, 1, qkv, QKV, s, wexp), "qkv matmul");
     } else {
-      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiPartial, qkv_splits, partials, QKV, s), "qkv matmul");
+      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiPartial, qkv_splits, partials, QKV, s, wexp), "qkv matmul");
       hip_check(launch_reduce_partials(partials, qkv_splits, M, QKV, qkv, QKV, s), "qkv reduce");
     }
     mark(2, false);
@@ -741,9 +750,9 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
       const int splits = gemm_splits(wt);
       mark(stage, true);
       if (splits == 1)
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s), "residual matmul");
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wexp), "residual matmul");
       else
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s), "residual matmul");
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wexp), "residual matmul");
       mark(stage, false);
       mark(stage + 1, true);
       if (splits == 1)
@@ -754,7 +763,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     };
     residual(attn, QW, w.o, w.ffn_norm, 4);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
-    hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s), "gate/up matmul");
+    hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
     residual(ffn, F, w.down, next, 8);
@@ -891,14 +900,19 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
     if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
     set_device(weight->ctx);
     hipStream_t s = (hipStream_t)stream;
+    if (algo < 0 || algo > 3) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+    const QWeight& w = weight->w;
     const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= 16);
-    if (algo < 0 || algo > 2) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+    const bool two_pass =
+        algo == NEMO_MATMUL_TWO_PASS || (algo == NEMO_MATMUL_AUTO && !gemv && gemm_two_pass(w, m, 1));
     if (gemv) {
       if (m > 16) fail(NEMO_ERR_INVALID, "GEMV takes m <= 16");
-      hip_check(launch_gemv(d_x, weight->w.k, weight->w, d_y, weight->w.n, m, (float*)weight->partials.get(), s),
-                "gemv");
+      hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)weight->partials.get(), s), "gemv");
+    } else if (two_pass) {
+      if (!weight->wexp) weight->wexp = dev_alloc((size_t)w.n * w.k * 2, "f16 weight expansion");
+      hip_check(launch_gemm_two_pass(d_x, w.k, w, m, d_y, w.n, (uint16_t*)weight->wexp.get(), s), "two-pass gemm");
     } else {
-      hip_check(launch_gemm(d_x, weight->w.k, weight->w, d_y, weight->w.n, m, s), "gemm");
+      hip_check(launch_gemm(d_x, w.k, w, d_y, w.n, m, s), "gemm");
     }
   });
 }

@@ -18,36 +18,35 @@ namespace nemo {
 
 typedef float float8v __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ uint32_t byte_of(const u32x4& v, int i) {
-  const uint32_t w = (i < 4) ? v.x : (i < 8) ? v.y : (i < 12) ? v.z : v.w;
-  return (w >> (8 * (i & 3))) & 0xffu;
-}
-
-// Scale and min of sub-block j (0..7) from the 12 packed bytes that follow
-// d and dmin (src/gguf/quantization.ts:11-17). `hdr` is the block's first 16
-// bytes, so scale byte i is byte 4 + i of hdr.
-__device__ __forceinline__ void q4k_scale_min(const u32x4& hdr, int j, uint32_t& sc, uint32_t& m) {
-  if (j < 4) {
-    sc = byte_of(hdr, 4 + j) & 63u;
-    m = byte_of(hdr, 8 + j) & 63u;
-  } else {
-    sc = (byte_of(hdr, 8 + j) & 15u) | ((byte_of(hdr, j) >> 6) << 4);
-    m = (byte_of(hdr, 8 + j) >> 4) | ((byte_of(hdr, 4 + j) >> 6) << 4);
-  }
-}
-
 // fp32 factors of group g (sub-blocks 2g, 2g+1): w = fmaf(dsc, q, ndm).
+// scaleAndMin (src/gguf/quantization.ts:11-17) on whole words, branch-free:
+// with the 12 scale bytes s[0..11] in hdr.y, hdr.z, hdr.w, sub-block j < 4
+// has scale s[j] & 63 and min s[j+4] & 63; sub-block j >= 4 has scale
+// (s[j+4] & 15) | (s[j-4] >> 6) << 4 and min (s[j+4] >> 4) | (s[j] >> 6) << 4.
+// Per byte, (x >> 6) << 4 is ((word >> 2) & 0x30).
 __device__ __forceinline__ void q4k_group_factors(const u32x4& hdr, int g, float& dsc0, float& ndm0, float& dsc1,
                                                   float& ndm1) {
   const float d = h2f((uint16_t)(hdr.x & 0xffffu));
   const float dmin = h2f((uint16_t)(hdr.x >> 16));
-  uint32_t sc, m;
-  q4k_scale_min(hdr, 2 * g, sc, m);
-  dsc0 = d * (float)sc;
-  ndm0 = -(dmin * (float)m);
-  q4k_scale_min(hdr, 2 * g + 1, sc, m);
-  dsc1 = d * (float)sc;
-  ndm1 = -(dmin * (float)m);
+  // Bitwise blend rather than a conditional: g is uniform, and a branch would
+  // split the GEMM's step into several basic blocks.
+  const uint32_t hi = 0u - (uint32_t)(g >> 1);
+  const uint32_t scw = ((hdr.y & 0x3f3f3f3fu) & ~hi) | (((hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u)) & hi);
+  const uint32_t mw =
+      ((hdr.z & 0x3f3f3f3fu) & ~hi) | ((((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u)) & hi);
+  const int sh = 16 * (g & 1);
+  dsc0 = d * (float)((scw >> sh) & 0xffu);
+  ndm0 = -(dmin * (float)((mw >> sh) & 0xffu));
+  dsc1 = d * (float)((scw >> (sh + 8)) & 0xffu);
+  ndm1 = -(dmin * (float)((mw >> (sh + 8)) & 0xffu));
+}
+
+// Hides a value's known bits from the optimizer so that byte extraction of a
+// masked word compiles to v_cvt_f32_ubyte{0..3} (one instruction per value)
+// rather than a bit-field extract followed by a conversion.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // Four packed bytes (one value per byte) -> four fp32 values scale*b + bias.
@@ -93,8 +92,8 @@ __device__ __forceinline__ void q4k_expand(const Q4KFetch& f, half8v* lo, half8v
   float vl[16], vh[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    bytes4_fma(words[i] & 0x0f0f0f0fu, dsc0, ndm0, vl + 4 * i);
-    bytes4_fma((words[i] >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh + 4 * i);
+    bytes4_fma(opaque(words[i] & 0x0f0f0f0fu), dsc0, ndm0, vl + 4 * i);
+    bytes4_fma(opaque((words[i] >> 4) & 0x0f0f0f0fu), dsc1, ndm1, vh + 4 * i);
   }
   lo[0] = to_half8(vl);
   lo[1] = to_half8(vl + 8);
@@ -142,8 +141,8 @@ __device__ __forceinline__ void q6k_expand(const Q6KFetch& f, half8v* lo, half8v
   for (int i = 0; i < 4; ++i) {
     const uint32_t q0 = ((la[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s0) & 0x03030303u) << 4);
     const uint32_t q1 = ((lb[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s1) & 0x03030303u) << 4);
-    bytes4_fma(q0, dsc0, -32.0f * dsc0, vl + 4 * i);
-    bytes4_fma(q1, dsc1, -32.0f * dsc1, vh + 4 * i);
+    bytes4_fma(opaque(q0), dsc0, -32.0f * dsc0, vl + 4 * i);
+    bytes4_fma(opaque(q1), dsc1, -32.0f * dsc1, vh + 4 * i);
   }
   lo[0] = to_half8(vl);
   lo[1] = to_half8(vl + 8);

@@ -1,60 +1,133 @@
-// Fused dequant + MFMA GEMM for gfx950: Y[M, N] = X[M, K] * W[N, K]^T with
-// W in Q4_K (GGUF blocks) or Q6_K (split layout), X f16, fp32 accumulate.
+// Dequant + MFMA GEMM for gfx950: Y[M, N] = X[M, K] * W[N, K]^T with W in
+// Q4_K (GGUF blocks) or Q6_K (split layout), X f16, fp32 accumulate.
 //
-// Workgroup tile BM x 128 x 64 (BM = 256 or 128), 256 threads = 4 waves.
-// Wave w owns rows [w*BM/4, (w+1)*BM/4) and all 128 columns, as a grid of
-// v_mfma_f32_32x32x16_f16 blocks (BM/128 x 4). The W tile (128 rows x 64
-// columns) is decoded once per workgroup into LDS and shared by the BM rows
-// of X; the X tile is copied to LDS. Global loads of step k+1 are issued
-// before the MFMAs of step k. LDS rows are padded to 72 halves (144 bytes) so
-// the 16-byte fragment reads of 32 consecutive rows hit distinct banks.
-//
-// Owning all 128 columns lets the gate/up projection finish SwiGLU in
-// registers: the plan stores gate_up with rows interleaved per 128-row tile
-// (64 gate rows, then the matching 64 up rows), so a lane holds g and u of
-// the same (token, feature) in blocks j and j+2.
+// Three kernels share the decode, the epilogues and the split-K contract:
+//  * gemm_kernel<BM>: BM x 128 x 64 tiles (BM 128 or 256), 4 waves, both
+//    operands staged in LDS through registers, W decoded in the kernel.
+//  * gemm_big_kernel: 256 x 256 x 64 tiles, 8 waves of 64 x 128, X copied
+//    global -> LDS directly, W decoded in the kernel (Q4_K, large problems).
+//  * expand_kernel + gemm_f16_kernel (two-pass): W expanded to f16 once per
+//    call, then 256 x 256 x 64 tiles with both operands copied global -> LDS.
+// Every wave owns whole 128-column groups, so the gate/up projection finishes
+// SwiGLU in registers: the plan stores gate_up with rows interleaved per
+// 128-row group (64 gate rows, then the matching 64 up rows), and a lane
+// holds g and u of the same (token, feature) in column blocks j and j+2.
 //
 // Split-K: blockIdx.z selects a contiguous K range; partial sums are written
 // as fp32 and summed in a fixed order by the consumer (deterministic). The
-// split count depends only on the weight's shape, never on M, so a token's
-// result does not depend on how many other tokens share the batch.
+// split count depends only on the weight's shape, never on M, and every row's
+// K order is the same in every kernel (sequential 16-column MFMA steps on the
+// same f16 operands), so all paths give identical bits and a
+// token's result does not depend on how many other tokens share the batch.
 #include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_quant.h"
 
 namespace nemo {
 
-constexpr int kBN = 128, kBK = 64, kLdsK = kBK + 8;
+constexpr int kBK = 64, kLdsK = kBK + 8;
+
+template <int TYPE>
+struct WFetch;
+template <>
+struct WFetch<kQ4_K> {
+  Q4KFetch f;
+  __device__ __forceinline__ void load(const QWeight& w, size_t rb, int row, int k0, int p) {
+    f = q4k_fetch(w, rb, row, k0, p);
+  }
+  __device__ __forceinline__ void expand(half8v* lo, half8v* hi) const { q4k_expand(f, lo, hi); }
+};
+template <>
+struct WFetch<kQ6_K> {
+  Q6KFetch f;
+  __device__ __forceinline__ void load(const QWeight& w, size_t rb, int row, int k0, int p) {
+    f = q6k_fetch(w, rb, row, k0, p);
+  }
+  __device__ __forceinline__ void expand(half8v* lo, half8v* hi) const { q6k_expand(f, lo, hi); }
+};
+
+// Epilogue for a wave owning MI x 4 blocks of 32 x 32 starting at (rbase0,
+// cbase): lane l, register r of block (i, j) is row rbase0 + 32i + 8(r/4) +
+// 4(l/32) + r%4, column cbase + 32j + l%32.
+template <int EPI, int MI>
+__device__ __forceinline__ void gemm_epilogue(const float16v (&acc)[MI][4], int rbase0, int cbase, int lane, int M,
+                                              int N, void* out, int ldo) {
+  const int rbase = rbase0 + 4 * (lane >> 5);
+  if constexpr (EPI == kEpiSwiGLU) {
+    // Columns j*32 + l%32 (j = 0, 1) of this wave's 128 are gate features
+    // cbase/2 + j*32 + l%32; columns 64 + j*32 + l%32 are their up rows.
+    // SwiGLU as src/webgpu/ops.ts:85-87 on the f16-rounded gate/up values.
+    uint16_t* y = (uint16_t*)out;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = (cbase >> 1) + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < M) {
+            const float g = (float)(half_t)acc[i][j][r];
+            const float u = (float)(half_t)acc[i][j + 2][r];
+            y[(size_t)row * ldo + col] = f2h(g / (1.0f + expf(-g)) * u);
+          }
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = cbase + j * 32 + (lane & 31);
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row >= M) continue;
+          if constexpr (EPI == kEpiStore)
+            ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
+          else
+            ((float*)out)[((size_t)blockIdx.z * M + row) * ldo + col] = acc[i][j][r];
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged tiles: BM x 128 x 64 (BM = 128 or 256), 4 waves along M, each
+// BM/4 x 128. Per K step every thread loads its share of X (8 threads per
+// row, 16 bytes each: coalesced 128-byte row segments) and the raw weight
+// bytes of its half row into registers; after the barrier it decodes, stores
+// both tiles to LDS (rows padded to 72 halves so fragment reads of 32
+// consecutive rows hit distinct banks), and the loads of the next step are
+// issued before the MFMAs of this one.
+// ---------------------------------------------------------------------------
 
 template <int TYPE, int BM, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w, int M,
                                                    int kchunk, void* __restrict__ out, int ldo) {
-  constexpr int WM = BM / 4, MI = WM / 32, XP = BM / 32;
+  constexpr int BN = 128, WM = BM / 4, MI = WM / 32, XP = BM / 32;
   __shared__ __attribute__((aligned(16))) half_t sA[BM * kLdsK];
-  __shared__ __attribute__((aligned(16))) half_t sB[kBN * kLdsK];
+  __shared__ __attribute__((aligned(16))) half_t sB[BN * kLdsK];
   const int N = w.n;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int kbeg = blockIdx.z * kchunk, kend = kbeg + kchunk;
   const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
 
-  // X loader: 8 threads per row (16 bytes each), 32 rows per pass.
   const int xr = tid >> 3, xc = (tid & 7) * 8;
   const uint16_t* xrow[XP];
 #pragma unroll
   for (int i = 0; i < XP; ++i) xrow[i] = x + (size_t)min(m0 + i * 32 + xr, M - 1) * ldx + xc;
-  // W loader: 2 threads per weight row.
   const int wr = tid >> 1, wp = tid & 1;
   const int wrow = min(n0 + wr, N - 1);
 
   u32x4 xa[XP];
-  Q4KFetch f4;
-  Q6KFetch f6;
+  WFetch<TYPE> wf;
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < XP; ++i) xa[i] = *(const u32x4*)(xrow[i] + k0);
-    if constexpr (TYPE == kQ4_K) f4 = q4k_fetch(w, row_bytes, wrow, k0, wp);
-    else f6 = q6k_fetch(w, row_bytes, wrow, k0, wp);
+    wf.load(w, row_bytes, wrow, k0, wp);
   };
 
   float16v acc[MI][4];
@@ -68,8 +141,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t* __restrict__ 
   fetch(kbeg);
   for (int k0 = kbeg; k0 < kend; k0 += kBK) {
     half8v lo[2], hi[2];
-    if constexpr (TYPE == kQ4_K) q4k_expand(f4, lo, hi);
-    else q6k_expand(f6, lo, hi);
+    wf.expand(lo, hi);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < XP; ++i) *(u32x4*)&sA[(i * 32 + xr) * kLdsK + xc] = xa[i];
@@ -94,54 +166,281 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t* __restrict__ 
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
   }
+  gemm_epilogue<EPI, MI>(acc, m0 + wave * WM, n0, lane, M, N, out, ldo);
+}
 
-  // D layout of a 32x32 block: lane l, register r -> row 8*(r/4) + 4*(l/32)
-  // + r%4, column l%32.
-  const int rbase = m0 + wave * WM + 4 * (lane >> 5);
-  if constexpr (EPI == kEpiSwiGLU) {
-    // Columns j*32 + l%32 (j = 0, 1) are gate features n0/2 + j*32 + l%32;
-    // columns 64 + j*32 + l%32 are their up rows. SwiGLU as
-    // src/webgpu/ops.ts:85-87 on the f16-rounded gate/up values.
-    uint16_t* y = (uint16_t*)out;
+// ---------------------------------------------------------------------------
+// Large tiles: 256 x 256 x 64, 8 waves (4 along M x 2 along N), each 64 x 128,
+// two waves per SIMD so one wave's decode overlaps the other's MFMAs.
+//  * X: each K step's 256 x 64 tile is copied HBM/L2 -> LDS by
+//    global_load_lds_dwordx4 (no registers, no VALU): one wave instruction
+//    moves 8 whole 128-byte row segments (8 lanes per row). In LDS a row is 8
+//    slots of 16 bytes; logical chunk c of row r sits in slot c ^ f(r), f(r)
+//    = (r & 7) ^ ((r >> 3) & 1), so A-fragment reads (32 rows, one chunk) hit
+//    distinct banks for 32- or 64-bank LDS.
+//  * W: two threads per weight row decode it into a padded LDS tile. Raw
+//    bytes use two register sets; the set for step s+3 is loaded right after
+//    the barrier that closes step s.
+// X and W tiles are double-buffered: the copy of step k+2 and the decode of
+// step k+1 run under the MFMAs of step k, and every global access has a
+// whole step to land before the vmcnt(0) that precedes the step's barrier.
+// LDS: 2 x 32 KB (X) + 2 x 36 KB (W) = 138 KB, dynamic.
+// ---------------------------------------------------------------------------
+
+constexpr int kBigBM = 256, kBigBN = 256;
+constexpr int kBigXStage = kBigBM * kBK * 2;    // bytes
+constexpr int kBigWStage = kBigBN * kLdsK * 2;  // bytes
+constexpr int kBigLds = 2 * kBigXStage + 2 * kBigWStage;
+
+__device__ __forceinline__ int xswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int TYPE, int EPI>
+__global__ __launch_bounds__(512) void gemm_big_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w, int M,
+                                                       int kchunk, void* __restrict__ out, int ldo) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* sX = smem;                             // [2][256 rows][128 B]
+  half_t* sW = (half_t*)(smem + 2 * kBigXStage);  // [2][256][72]
+  constexpr int MI = 2;
+  const int N = w.n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int m0 = blockIdx.y * kBigBM, n0 = blockIdx.x * kBigBN;
+  const int kbeg = blockIdx.z * kchunk;
+  const int nsteps = kchunk / kBK;
+  const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
+
+  // X copy: wave w moves rows [32w, 32w + 32) in 4 instructions of 8 rows;
+  // lane l -> row R + l/8, slot l%8, which holds logical chunk
+  // (l%8) ^ f(row).
+  const uint16_t* xsrc[4];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * wave + 8 * i + (lane >> 3);
+    const int c = (lane & 7) ^ xswz(r);
+    xsrc[i] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * c;
+  }
+  auto copy_x = [&](int stage, int k0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = (n0 >> 1) + j * 32 + (lane & 31);
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + k0),
+                                       (lds_void*)(sX + stage * kBigXStage + (32 * wave + 8 * i) * 128), 16, 0, 0);
+  };
+
+  // W decode: 2 threads per weight row.
+  const int wr = tid >> 1, wp = tid & 1;
+  const int wrow = min(n0 + wr, N - 1);
+  WFetch<TYPE> ra, rb;  // raw bytes of even / odd steps
+  auto store_w = [&](const WFetch<TYPE>& f, int stage) {
+    half8v lo[2], hi[2];
+    f.expand(lo, hi);
+    half_t* brow = sW + stage * (kBigBN * kLdsK) + wr * kLdsK;
+    *(half8v*)(brow + 16 * wp) = lo[0];
+    *(half8v*)(brow + 16 * wp + 8) = lo[1];
+    *(half8v*)(brow + 32 + 16 * wp) = hi[0];
+    *(half8v*)(brow + 32 + 16 * wp + 8) = hi[1];
+  };
+
+  float16v acc[MI][4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row < M) {
-            const float g = (float)(half_t)acc[i][j][r];
-            const float u = (float)(half_t)acc[i][j + 2][r];
-            y[(size_t)row * ldo + col] = f2h(g / (1.0f + expf(-g)) * u);
-          }
-        }
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto mfma_step = [&](int stage) {
+    const uint8_t* xs = sX + stage * kBigXStage;
+    const half_t* ws = sW + stage * (kBigBN * kLdsK);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int c = 2 * ks + (lane >> 5);
+      half8v af[MI], bf[4];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * 64 + i * 32 + (lane & 31);
+        af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
       }
-  } else {
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+      for (int j = 0; j < 4; ++j) bf[j] = *(const half8v*)(ws + (wn * 128 + j * 32 + (lane & 31)) * kLdsK + 8 * c);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // One MFMA pair, then some of the decode's VALU work and LDS traffic.
+  auto interleave = [] {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+    }
+  };
+
+  auto kat = [&](int s) { return kbeg + min(s, nsteps - 1) * kBK; };
+  copy_x(0, kat(0));
+  ra.load(w, row_bytes, wrow, kat(0), wp);
+  copy_x(1, kat(1));
+  rb.load(w, row_bytes, wrow, kat(1), wp);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  store_w(ra, 0);
+  ra.load(w, row_bytes, wrow, kat(2), wp);
+  __syncthreads();
+  for (int s = 0; s < nsteps; s += 2) {
+    // even step s: stage 0 holds X(s), W(s); rb holds raw(s+1); ra is
+    // receiving raw(s+2).
+    mfma_step(0);
+    store_w(rb, 1);
+    interleave();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    copy_x(0, kat(s + 2));
+    rb.load(w, row_bytes, wrow, kat(s + 3), wp);
+    // odd step s+1: stage 1 holds X(s+1), W(s+1); ra holds raw(s+2).
+    mfma_step(1);
+    store_w(ra, 0);
+    interleave();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    copy_x(1, kat(s + 3));
+    ra.load(w, row_bytes, wrow, kat(s + 4), wp);
+  }
+  // The last (clamped, unused) copies must land before the workgroup's LDS
+  // is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  gemm_epilogue<EPI, MI>(acc, m0 + wm * 64, n0 + wn * 128, lane, M, N, out, ldo);
+}
+
+// ---------------------------------------------------------------------------
+// Two-pass path for large batches. A bandwidth-bound pre-pass expands W to an
+// f16 [n][k] matrix with the same decoders the fused kernels use (identical
+// f16 values), then gemm_f16_kernel runs 256 x 256 x 64 tiles with both
+// operands copied global -> LDS by global_load_lds_dwordx4 into the swizzled
+// layout described above, 8 waves of 64 x 128. Each wave issues the same MFMA
+// sequence per output element as the fused kernels (16-column steps in K
+// order), so the two paths give bit-identical results.
+// LDS: 2 x 32 KB (X) + 2 x 32 KB (W) = 128 KB, dynamic.
+// ---------------------------------------------------------------------------
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __restrict__ out) {
+  // Thread t: row t / (k/32), 64-column chunk (t % (k/32)) / 2, part t % 2.
+  const int per_row = w.k >> 5;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)w.n * per_row) return;
+  const int row = (int)(t / per_row), i = (int)(t % per_row);
+  const int k0 = 64 * (i >> 1), p = i & 1;
+  WFetch<TYPE> f;
+  f.load(w, qweight_row_bytes(TYPE, w.k), row, k0, p);
+  half8v lo[2], hi[2];
+  f.expand(lo, hi);
+  uint16_t* dst = out + (size_t)row * w.k + k0 + 16 * p;
+  *(half8v*)dst = lo[0];
+  *(half8v*)(dst + 8) = lo[1];
+  *(half8v*)(dst + 32) = hi[0];
+  *(half8v*)(dst + 40) = hi[1];
+}
+
+constexpr int kF16Lds = 4 * kBigXStage;
+
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                       const uint16_t* __restrict__ wt, int N, int K, int M,
+                                                       int kchunk, void* __restrict__ out, int ldo) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* sX = smem;                   // [2][256 rows][128 B]
+  uint8_t* sW = smem + 2 * kBigXStage;  // [2][256 rows][128 B]
+  constexpr int MI = 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int m0 = blockIdx.y * kBigBM, n0 = blockIdx.x * kBigBN;
+  const int kbeg = blockIdx.z * kchunk;
+  const int nsteps = kchunk / kBK;
+
+  // Wave w copies rows [32w, 32w + 32) of both tiles, 8 rows per instruction;
+  // lane l -> row R + l/8, slot l%8 holding logical chunk (l%8) ^ f(row).
+  const uint16_t* xsrc[4];
+  const uint16_t* wsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * wave + 8 * i + (lane >> 3);
+    const int c = (lane & 7) ^ xswz(r);
+    xsrc[i] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * c;
+    wsrc[i] = wt + (size_t)min(n0 + r, N - 1) * K + 8 * c;
+  }
+  auto copy = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + k0),
+                                       (lds_void*)(sX + stage * kBigXStage + (32 * wave + 8 * i) * 128), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + k0),
+                                       (lds_void*)(sW + stage * kBigXStage + (32 * wave + 8 * i) * 128), 16, 0, 0);
+    }
+  };
+
+  float16v acc[MI][4];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto mfma_step = [&](int stage) {
+    const uint8_t* xs = sX + stage * kBigXStage;
+    const uint8_t* ws = sW + stage * kBigXStage;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int c = 2 * ks + (lane >> 5);
+      half8v af[MI], bf[4];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * 64 + i * 32 + (lane & 31);
+        af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int col = n0 + j * 32 + (lane & 31);
-        if (col >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row >= M) continue;
-          if constexpr (EPI == kEpiStore)
-            ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
-          else
-            ((float*)out)[((size_t)blockIdx.z * M + row) * ldo + col] = acc[i][j][r];
-        }
+        const int r = wn * 128 + j * 32 + (lane & 31);
+        bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
       }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // The copies of step s+2 are issued right after the barrier that frees
+  // their stage and have the whole of step s+1 to land. Loads complete in
+  // order: vmcnt(8) leaves the 8 copies of the newer stage in flight.
+  auto kat = [&](int s) { return kbeg + min(s, nsteps - 1) * kBK; };
+  copy(0, kat(0));
+  copy(1, kat(1));
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __syncthreads();
+  for (int s = 0; s < nsteps; s += 2) {
+    mfma_step(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    copy(0, kat(s + 2));
+    mfma_step(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    copy(1, kat(s + 3));
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  gemm_epilogue<EPI, MI>(acc, m0 + wm * 64, n0 + wn * 128, lane, M, N, out, ldo);
 }
 
 int gemm_splits(const QWeight& w) {
   // Narrow projections (N = hidden) give too few column tiles to fill 256
   // CUs: split K into chunks of at least 1024 columns, at most 4 ways.
-  const int ntiles = (w.n + kBN - 1) / kBN;
+  const int ntiles = (w.n + 127) / 128;
   const int kblocks = w.k / 256;
   if (ntiles >= 24) return 1;
   int s = 1;
@@ -149,33 +448,87 @@ int gemm_splits(const QWeight& w) {
   return s;
 }
 
+enum GemmVariant { kVarBig = 0, kVarLds128 = 1, kVarLds256 = 2 };
+
 template <int TYPE, int EPI>
-static void launch_typed(int bm, dim3 grid, const uint16_t* x, int ldx, const QWeight& w, int m, int kchunk, void* out,
-                         int ldo, hipStream_t s) {
-  if (bm == 256) gemm_kernel<TYPE, 256, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
-  else gemm_kernel<TYPE, 128, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
+static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx, const QWeight& w, int kchunk,
+                         void* out, int ldo, hipStream_t s) {
+  if (var == kVarBig) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+      (void)hipFuncSetAttribute((const void*)gemm_big_kernel<TYPE, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kBigLds);
+      configured = true;
+    }
+    dim3 grid((w.n + kBigBN - 1) / kBigBN, (m + kBigBM - 1) / kBigBM, splits);
+    gemm_big_kernel<TYPE, EPI><<<grid, 512, kBigLds, s>>>(x, ldx, w, m, kchunk, out, ldo);
+  } else if (var == kVarLds256) {
+    dim3 grid((w.n + 127) / 128, (m + 255) / 256, splits);
+    gemm_kernel<TYPE, 256, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
+  } else {
+    dim3 grid((w.n + 127) / 128, (m + 127) / 128, splits);
+    gemm_kernel<TYPE, 128, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
+  }
+}
+
+// Fused-kernel choice, from measurements of the encoder's shapes: the 256 x
+// 256 Q4_K kernel once it alone gives every CU a workgroup; Q6_K decodes more
+// VALU work per weight and does best on the 4-wave LDS-staged tiles.
+static int gemm_variant(const QWeight& w, int m, int splits) {
+  const int ntiles = (w.n + 127) / 128;
+  if (w.type == kQ4_K && w.n % kBigBN == 0 && ((m + kBigBM - 1) / kBigBM) * (w.n / kBigBN) * splits >= 256)
+    return kVarBig;
+  if (w.type == kQ6_K && m >= 512) return kVarLds256;
+  return (m >= 512 && ((m + 255) / 256) * ntiles * splits >= 512) ? kVarLds256 : kVarLds128;
+}
+
+bool gemm_two_pass(const QWeight& w, int m, int splits) {
+  // The f16 GEMM runs 256 x 256 tiles: worth the expansion pass once the
+  // tiles alone give every CU a workgroup.
+  return w.n % kBigBN == 0 && ((m + kBigBM - 1) / kBigBM) * (w.n / kBigBN) * splits >= 256;
+}
+
+static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
+                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream) {
+  if (epilogue == kEpiSwiGLU && w.n % kBigBN) return hipErrorInvalidValue;
+  const int64_t threads = (int64_t)w.n * (w.k / 32);
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  if (w.type == kQ4_K) expand_kernel<kQ4_K><<<blocks, 256, 0, stream>>>(w, wexp);
+  else expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
+  const int kchunk = w.k / splits;
+  dim3 grid((w.n + kBigBN - 1) / kBigBN, (m + kBigBM - 1) / kBigBM, splits);
+  auto launch = [&](auto kernel) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+      (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kF16Lds);
+      configured = true;
+    }
+    kernel<<<grid, 512, kF16Lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
+  };
+  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore>);
+  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial>);
+  else launch(gemm_f16_kernel<kEpiSwiGLU>);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream) {
+                          int ldo, hipStream_t stream, uint16_t* wexp) {
   if (m <= 0) return hipSuccess;
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
   if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
-  if (epilogue == kEpiSwiGLU && w.n % kBN) return hipErrorInvalidValue;
-  const int ntiles = (w.n + kBN - 1) / kBN;
-  const int bm = (m >= 512 && ((m + 255) / 256) * ntiles * splits >= 512) ? 256 : 128;
-  dim3 grid(ntiles, (m + bm - 1) / bm, splits);
+  if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
+  if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
-#define NEMO_LAUNCH(T)                                                                           \
-  if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(bm, grid, x, ldx, w, m, kchunk, out, ldo, stream);   \
-  else if (epilogue == kEpiPartial) launch_typed<T, kEpiPartial>(bm, grid, x, ldx, w, m, kchunk, out, ldo, stream); \
-  else launch_typed<T, kEpiSwiGLU>(bm, grid, x, ldx, w, m, kchunk, out, ldo, stream);
+  if (wexp && gemm_two_pass(w, m, splits)) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream);
+  const int var = gemm_variant(w, m, splits);
+#define NEMO_LAUNCH(T)                                                                                              \
+  if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
+  else if (epilogue == kEpiPartial) launch_typed<T, kEpiPartial>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream); \
+  else launch_typed<T, kEpiSwiGLU>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);
   if (w.type == kQ4_K) {
     NEMO_LAUNCH(kQ4_K)
-  } else if (w.type == kQ6_K) {
-    NEMO_LAUNCH(kQ6_K)
   } else {
-    return hipErrorInvalidValue;
+    NEMO_LAUNCH(kQ6_K)
   }
 #undef NEMO_LAUNCH
   return hipGetLastError();
@@ -183,6 +536,13 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
 
 hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, hipStream_t stream) {
   return launch_gemm_ex(x, ldx, w, m, kEpiStore, 1, y, ldy, stream);
+}
+
+hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, uint16_t* y, int ldy,
+                                uint16_t* wexp, hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
+  return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream);
 }
 
 }  // namespace nemo

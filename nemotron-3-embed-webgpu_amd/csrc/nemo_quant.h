@@ -42,13 +42,24 @@ enum GemmEpilogue : int {
 hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
                        hipStream_t stream);
 
+// launch_gemm through the two-pass path: W expanded into `wexp` (n * k
+// halves), then the f16 MFMA GEMM. Bit-identical to launch_gemm.
+hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, uint16_t* y, int ldy,
+                                uint16_t* wexp, hipStream_t stream);
+
 // The K-split count the encoder uses for `w`: a function of the weight's
 // shape only.
 int gemm_splits(const QWeight& w);
 
-// The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial.
+// Whether launch_gemm_ex, given scratch, expands `w` to f16 before an f16 x
+// f16 MFMA GEMM (large batches) rather than decoding inside the GEMM.
+bool gemm_two_pass(const QWeight& w, int m, int splits);
+
+// The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial. With
+// `wexp` (room for n * k halves) large problems take the two-pass path, whose
+// results are bit-identical to the fused kernels'.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream);
+                          int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
 
 // y[m, n] = f16(sum over s of partials[s][m][n]) in split order.
 hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,

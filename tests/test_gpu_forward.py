@@ -84,6 +84,28 @@ def test_missing_tensor_is_named(torch_cuda):
         rt.NemotronHipModel(tensors, dims=dims)
 
 
+def test_config_dims_full_batch_matches_oracle(torch_cuda):
+    """The benchmark's shapes (config dims, 16 requests x 150 tokens) through
+    two layers (merge after the first): every projection kernel variant the
+    16-layer pass uses at this batch, including the 256 x 256 SwiGLU tiles."""
+    dims = rt.config_dims()
+    dims.layers, dims.merge_after_layer, dims.vocab = 2, 1, 8192
+    model = rt.NemotronHipModel(None, dims=dims, synthetic_seed=2024)
+    tensors = {}
+    for name in ["token_embd.weight", "output_norm.weight"] + [f"blk.{l}.{t}.weight" for l in range(2) for t in (
+            "attn_qkv", "attn_output", "ffn_gate_up", "ffn_down", "attn_norm", "ffn_norm")]:
+        typ, d, data = model.get_tensor(name)
+        tensors[name] = (typ, [x for x in d if x != 1] or [1], data)
+    om = synth.oracle_model(dims, tensors)
+    ids = synth.randint(77, 16 * 150, 2, dims.vocab).astype(np.uint32)
+    ids[::150] = 1
+    got = model.createPlan(16, 150).run_sync(ids, [150] * 16)
+    for b in (0, 7, 15):
+        ref = oracle.forward_request(om, ids[b * 150:(b + 1) * 150].astype(np.int64))
+        c = _cos(got[b], ref)
+        assert c >= 0.9999, f"request {b}: cosine {c:.6f}"
+
+
 def test_synthetic_model_readback_matches_oracle(torch_cuda):
     """Device-synthesized weights read back through the ABI drive the oracle
     to the same embedding (config dims, 2 layers, 40 tokens)."""

@@ -119,6 +119,61 @@ def test_matmul_vs_oracle(torch_cuda, type_, m, n, k, algo):
     _check_matmul(y, x16, oracle.dequantize(type_, raw).reshape(n, k))
 
 
+@pytest.mark.parametrize("type_,m,n,k", [
+    (12, 2400, 16384, 2048),   # the gate/up shape of 16 x 150 tokens: 256 x 256 LDS-copy tiles
+    (14, 4096, 8192, 2048),
+])
+def test_matmul_large_tiles_vs_oracle(torch_cuda, type_, m, n, k):
+    """Large problems take the 256 x 256 fused Q4_K kernel and the 256-row
+    Q6_K tiles; checked on a seeded sample of 512 columns (all rows) against
+    the float64 oracle."""
+    torch = torch_cuda
+    seed = 4001 + n
+    raw = (synth.random_q4k if type_ == 12 else synth.random_q6k)(seed, n * k // 256)
+    x16 = synth.normal(seed + 7, m * k).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(type_, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    dy = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    w.matmul(dx.data_ptr(), m, dy.data_ptr(), _lib.MATMUL_GEMM)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().view(np.float16)
+    cols = np.sort(synth.randint(seed + 9, 512, 0, n))
+    row_bytes = k // 256 * (144 if type_ == 12 else 210)
+    w_sample = np.concatenate([oracle.dequantize(type_, raw[c * row_bytes:(c + 1) * row_bytes]).reshape(1, k)
+                               for c in cols])
+    _check_matmul(y[:, cols], x16, w_sample)
+
+
+@pytest.mark.parametrize("type_,m,n,k", [
+    (12, 2400, 16384, 2048),   # gate/up at 16 x 150 tokens
+    (14, 2400, 2048, 8192),    # down
+    (12, 333, 200, 768),       # ragged rows and columns: clamped tile edges
+    (14, 70, 384, 512),
+])
+def test_two_pass_bit_identical_to_fused(torch_cuda, type_, m, n, k):
+    """The two-pass GEMM (expand W to f16, then an f16 MFMA GEMM) issues the
+    same f16 operands in the same MFMA order as the fused kernels: results
+    agree bit for bit, and match the oracle."""
+    torch = torch_cuda
+    seed = 5003 + m + n
+    raw = (synth.random_q4k if type_ == 12 else synth.random_q6k)(seed, n * k // 256)
+    x16 = synth.normal(seed + 7, m * k).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(type_, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    fused = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    two = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    w.matmul(dx.data_ptr(), m, fused.data_ptr(), _lib.MATMUL_GEMM)
+    w.matmul(dx.data_ptr(), m, two.data_ptr(), _lib.MATMUL_TWO_PASS)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two)
+    y = two.cpu().numpy().view(np.float16)
+    cols = np.sort(synth.randint(seed + 9, min(n, 256), 0, n))
+    row_bytes = k // 256 * (144 if type_ == 12 else 210)
+    w_sample = np.concatenate([oracle.dequantize(type_, raw[c * row_bytes:(c + 1) * row_bytes]).reshape(1, k)
+                               for c in cols])
+    _check_matmul(y[:, cols], x16, w_sample)
+
+
 def test_matmul_rejects_bad_shapes(torch_cuda):
     raw = synth.random_q4k(1, 2)
     with pytest.raises(rt.NemoError, match="divisible by 256"):
