@@ -1,0 +1,147 @@
+'use strict';
+// The HIP runtime behind the reference's EmbeddingRuntime interface
+// (src/webgpu/embedding-engine.ts:7-14): a model that createPlan()s execution
+// plans whose run(ids, lengths) resolves to one L2-normalised Float32Array
+// per request, computed by libnemo on an MI355X through the Node-API addon.
+// Mirrors NemotronWebGPUModel / NemotronExecutionPlan (src/webgpu/model.ts).
+const { native } = require('./native');
+const { isPrepackedModel, PREPACKED_STORAGE_COMPACT } = require('./prepacked');
+
+const GGMLType = Object.freeze({ F32: 0, F16: 1, Q4_0: 2, Q4_K: 12, Q6_K: 14 });
+const NEMO_ERR_UNSUPPORTED = 5;
+
+/** src/webgpu/model.ts:30-32 */
+function contextualMergedLength(sequence) {
+  return Math.max(1, Math.ceil(sequence * 0.64));
+}
+
+/** The reference model's constants (src/webgpu/model.ts:19-28). */
+function referenceDims() {
+  return native().dimsReference();
+}
+
+/** The benchmark configuration's shape: 32 query heads x 64, FFN 8192. */
+function configDims() {
+  return Object.assign(referenceDims(), { qHeads: 32, kvHeads: 8, headDim: 64, intermediate: 8192 });
+}
+
+/** Replaces requestWebGPUDevice (src/webgpu/device.ts:6-24). */
+class HipDevice {
+  constructor(index) {
+    this.index = index === undefined ? 0 : index;
+    this.handle = native().init(this.index);
+  }
+
+  destroy() {
+    if (!this.destroyed) native().shutdown(this.handle);
+    this.destroyed = true;
+  }
+}
+
+function requestHipDevice(index) {
+  return new HipDevice(index);
+}
+
+function unsupported(message) {
+  const error = new Error(message);
+  error.status = NEMO_ERR_UNSUPPORTED;
+  return error;
+}
+
+/**
+ * new NemotronHipModel(device, source, { dims, embeddingType })
+ * source: a PrepackedModel (parsePrepackedModel) with raw tensors, a
+ * GGUF-like { tensors: Map(name -> { dimensions, type, byteOffset,
+ * byteLength }), buffer }, or { synthetic: seed } for seeded synthetic weights.
+ */
+class NemotronHipModel {
+  constructor(device, source, options) {
+    const opts = options || {};
+    this.device = device;
+    this.dims = Object.assign(referenceDims(), opts.dims || {});
+    // No per-binding storage cap on HIP: the engine's storage split never triggers.
+    this.maxStorageBufferBindingSize = undefined;
+    const addon = native();
+    this.handle = addon.modelCreate(device.handle, this.dims);
+    try {
+      if (source && source.synthetic !== undefined) {
+        addon.modelSynthesize(this.handle, source.synthetic, opts.embeddingType === undefined ? GGMLType.F16 : opts.embeddingType);
+      } else {
+        if (!source || !(source.tensors instanceof Map)) throw new TypeError('model source must hold a tensors Map');
+        for (const tensor of source.tensors.values()) {
+          if (isPrepackedModel(source) && tensor.storage === PREPACKED_STORAGE_COMPACT) {
+            throw unsupported(`${tensor.name}: compact Q4_0 tile32 matrices are not supported by this build`);
+          }
+          const bytes = new Uint8Array(source.buffer, tensor.byteOffset, tensor.byteLength);
+          addon.modelSetTensor(this.handle, tensor.name, tensor.type, tensor.dimensions, bytes);
+        }
+      }
+      addon.modelFinalize(this.handle);
+    } catch (error) {
+      addon.modelDestroy(this.handle);
+      this.destroyed = true;
+      throw error;
+    }
+  }
+
+  createPlan(batch, sequence) {
+    return new NemotronHipPlan(this, batch, sequence);
+  }
+
+  /** Fails while plans of this model are alive (destroy them first). */
+  destroy() {
+    if (!this.destroyed) native().modelDestroy(this.handle);
+    this.destroyed = true;
+  }
+}
+
+function asU32(values) {
+  return values instanceof Uint32Array ? values : Uint32Array.from(values);
+}
+
+/** NemotronExecutionPlan (src/webgpu/model.ts:58-234). */
+class NemotronHipPlan {
+  constructor(model, batch, inputSequence) {
+    this.model = model;
+    this.batch = batch;
+    this.inputSequence = inputSequence;
+    this.sequence = contextualMergedLength(inputSequence);
+    this.handle = native().planCreate(model.handle, batch, inputSequence);
+  }
+
+  /** src/webgpu/model.ts:146-176: batch fresh Float32Array(hidden), in input order. */
+  run(ids, sequenceLengths) {
+    const hidden = this.model.dims.hidden;
+    let pending;
+    try {
+      pending = native().planRun(this.handle, asU32(ids), asU32(sequenceLengths), hidden);
+    } catch (error) {
+      return Promise.reject(error);
+    }
+    return pending.then((flat) => {
+      const out = [];
+      for (let b = 0; b < this.batch; b += 1) out.push(flat.slice(b * hidden, (b + 1) * hidden));
+      return out;
+    });
+  }
+
+  /** src/webgpu/model.ts:178-224: milliseconds per stage name, summed over layers. */
+  profile(ids, sequenceLengths) {
+    try {
+      return Promise.resolve(native().planProfile(this.handle, asU32(ids), asU32(sequenceLengths)));
+    } catch (error) {
+      return Promise.reject(error);
+    }
+  }
+
+  /** src/webgpu/model.ts:141-144. Later calls on the plan fail with 'plan was destroyed'. */
+  destroy() {
+    if (!this.destroyed) native().planDestroy(this.handle);
+    this.destroyed = true;
+  }
+}
+
+module.exports = {
+  GGMLType, contextualMergedLength, referenceDims, configDims, HipDevice, requestHipDevice, NemotronHipModel,
+  NemotronHipPlan,
+};
