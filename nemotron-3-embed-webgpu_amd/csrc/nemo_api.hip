@@ -600,6 +600,11 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
         if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
       }
     }
+    // Passes of at most 16 tokens take the GEMV, whose split counts differ.
+    const size_t small_m = std::min<size_t>(tf, 16);
+    for (const LayerWeights& w : model->layers)
+      for (const QWeight* q : {&w.qkv, &w.o, &w.gate_up, &w.down})
+        partial_floats = std::max(partial_floats, (size_t)gemv_splits(*q) * small_m * q->n);
     if (partial_floats) p->partials = dev_alloc(partial_floats * 4, "split-K partial sums");
     // f16 expansion of the largest matrix that takes the two-pass GEMM.
     size_t wexp_halves = 0;
@@ -730,8 +735,13 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     uint16_t* norm = full ? norm_full : norm_red;
     const LayerWeights& w = m->layers[l];
     mark(2, true);
+    // At most 16 tokens: the split-K GEMV (HBM-bound; the MFMA tiles would
+    // leave most CUs idle). Its results are independent of M too.
+    const bool small = M <= 16;
     const int qkv_splits = gemm_splits(w.qkv);
-    if (qkv_splits == 1) {
+    if (small) {
+      hip_check(launch_gemv_ex(norm, H, w.qkv, M, kEpiStore, qkv, QKV, partials, s), "qkv gemv");
+    } else if (qkv_splits == 1) {
       hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiStore, 1, qkv, QKV, s, wexp), "qkv matmul");
     } else {
       hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiPartial, qkv_splits, partials, QKV, s, wexp), "qkv matmul");
@@ -747,9 +757,13 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
     auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
-      const int splits = gemm_splits(wt);
+      const int splits = small ? gemv_splits(wt) : gemm_splits(wt);
       mark(stage, true);
-      if (splits == 1)
+      if (small)
+        hip_check(launch_gemv_ex(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial,
+                                 splits == 1 ? (void*)delta : (void*)partials, H, nullptr, s),
+                  "residual gemv");
+      else if (splits == 1)
         hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wexp), "residual matmul");
       else
         hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wexp), "residual matmul");
@@ -763,7 +777,10 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     };
     residual(attn, QW, w.o, w.ffn_norm, 4);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
-    hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
+    if (small)
+      hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
+    else
+      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
     residual(ffn, F, w.down, next, 8);

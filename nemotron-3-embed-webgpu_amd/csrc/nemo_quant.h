@@ -68,8 +68,17 @@ hipError_t launch_reduce_partials(const float* partials, int splits, int m, int 
 // Small-M path (m <= 16): split-K wavefront GEMV with a deterministic
 // reduction through `partials` (float, at least gemv_partials_floats()).
 size_t gemv_partials_floats(const QWeight& w, int m);
+// The GEMV's K-split count: a function of the weight's shape only.
+int gemv_splits(const QWeight& w);
 hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
                        float* partials, hipStream_t stream);
+
+// The GEMV with the GEMM's epilogues (m <= 16): kEpiStore as launch_gemv;
+// kEpiPartial writes [gemv_splits(w)][m][n] fp32 sums to `out` (ldo == n);
+// kEpiSwiGLU sums into `partials` (room for gemv_splits(w) * m * n floats),
+// then applies SwiGLU over the 128-row interleaved gate/up columns.
+hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, void* out, int ldo,
+                          float* partials, hipStream_t stream);
 
 // Decode raw GGUF blocks (Q4_K 144 B, Q6_K 210 B, Q4_0 18 B) to float32 and/or
 // f16 (either output may be null). n_blocks consecutive blocks.

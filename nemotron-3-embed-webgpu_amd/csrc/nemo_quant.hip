@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_q_kernel(const uint16_t*
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * kq + i;
     if (m >= M) continue;
-    if (gridDim.y == 1) y[(size_t)m * ldy + col] = f2h(acc[i]);
+    if (partials == nullptr) y[(size_t)m * ldy + col] = f2h(acc[i]);
     else partials[((size_t)blockIdx.y * M + m) * N + col] = acc[i];
   }
 }
@@ -119,7 +119,30 @@ hipError_t launch_reduce_partials(const float* partials, int splits, int m, int 
   return hipGetLastError();
 }
 
-static int gemv_splits(const QWeight& w) {
+// SwiGLU over split-K partials of the gate/up projection, whose rows are
+// interleaved per 128-row group (64 gate rows, then the matching 64 up rows):
+// feature f reads columns 128 (f / 64) + f % 64 (g) and that + 64 (u). Same
+// arithmetic as the GEMM's SwiGLU epilogue (src/webgpu/ops.ts:85-87 on the
+// f16-rounded g and u).
+__global__ void reduce_swiglu_kernel(const float* __restrict__ partials, int splits, int M, int N,
+                                     uint16_t* __restrict__ y, int ldy) {
+  const int F = N / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)M * F) return;
+  const int m = (int)(idx / F), f = (int)(idx % F);
+  const int gc = 128 * (f >> 6) + (f & 63);
+  float gs = 0.f, us = 0.f;
+  for (int i = 0; i < splits; ++i) {
+    const float* row = partials + ((size_t)i * M + m) * N;
+    gs += row[gc];
+    us += row[gc + 64];
+  }
+  const float g = (float)(half_t)gs;
+  const float u = (float)(half_t)us;
+  y[(size_t)m * ldy + f] = f2h(g / (1.0f + expf(-g)) * u);
+}
+
+int gemv_splits(const QWeight& w) {
   // Enough waves to keep every SIMD streaming: target >= 4096 waves.
   const int col_waves = (w.n + 15) / 16;
   const int blocks = w.k / 256;
@@ -141,13 +164,38 @@ hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
   const int kchunk = w.k / splits;
   if (splits > 1 && partials == nullptr) return hipErrorInvalidValue;
   dim3 grid((w.n + 16 * kGemvWaves - 1) / (16 * kGemvWaves), splits);
+  float* p = splits > 1 ? partials : nullptr;
   if (w.type == kQ4_K)
-    gemv_q_kernel<kQ4_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, partials, y, ldy);
+    gemv_q_kernel<kQ4_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, y, ldy);
   else if (w.type == kQ6_K)
-    gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, partials, y, ldy);
+    gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, y, ldy);
   else
     return hipErrorInvalidValue;
   if (splits > 1) return launch_reduce_partials(partials, splits, m, w.n, y, ldy, stream);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, void* out, int ldo,
+                          float* partials, hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  if (m > 16 || (w.type != kQ4_K && w.type != kQ6_K)) return hipErrorInvalidValue;
+  if (epilogue == kEpiStore) return launch_gemv(x, ldx, w, (uint16_t*)out, ldo, m, partials, stream);
+  const int splits = gemv_splits(w);
+  const int kchunk = w.k / splits;
+  dim3 grid((w.n + 16 * kGemvWaves - 1) / (16 * kGemvWaves), splits);
+  // kEpiPartial: the caller's buffer receives [splits][m][n] fp32 sums;
+  // kEpiSwiGLU: sums go to `partials`, then the SwiGLU reduction.
+  float* p = epilogue == kEpiPartial ? (float*)out : partials;
+  if (p == nullptr || (epilogue == kEpiPartial && ldo != w.n)) return hipErrorInvalidValue;
+  if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
+  if (w.type == kQ4_K)
+    gemv_q_kernel<kQ4_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, nullptr, 0);
+  else
+    gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, nullptr, 0);
+  if (epilogue == kEpiSwiGLU) {
+    const int64_t total = (int64_t)m * (w.n / 2);
+    reduce_swiglu_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(p, splits, m, w.n, (uint16_t*)out, ldo);
+  }
   return hipGetLastError();
 }
 

@@ -20,9 +20,11 @@ def _rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-@pytest.mark.parametrize("hd,emb,F", [(64, 1, 512), (128, 1, 512), (64, 14, 512), (128, 14, 512),
-                                      (64, 1, 4096)])  # F 4096: the down projection splits K four ways
-def test_one_layer_stages(torch_cuda, hd, emb, F):
+@pytest.mark.parametrize("hd,emb,F,n", [(64, 1, 512, 37), (128, 1, 512, 37), (64, 14, 512, 37), (128, 14, 512, 37),
+                                        (64, 1, 4096, 37),   # F 4096: the down projection splits K four ways
+                                        (64, 1, 4096, 12),   # at most 16 tokens: every projection on the GEMV
+                                        (128, 14, 512, 12)])
+def test_one_layer_stages(torch_cuda, hd, emb, F, n):
     H, V = 256, 300
     Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
     dims = rt.make_dims(hidden=H, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=F, layers=1, vocab=V,
@@ -30,7 +32,6 @@ def test_one_layer_stages(torch_cuda, hd, emb, F):
     tensors = synth.model_tensors(dims, seed=500 + hd + emb, embedding_type=emb)
     model = rt.NemotronHipModel(tensors, dims=dims)
     om = synth.oracle_model(dims, tensors)
-    n = 37
     seq = np.array([1] + list(synth.randint(41, n - 1, 2, V)), dtype=np.uint32)
     plan = model.createPlan(1, n)
     got = plan.run_sync(seq, [n])[0]
