@@ -34,6 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, "nemotron-3-embed-webgpu_amd"))
 BATCH, TOKENS = 16, 150
 SEED = 1003
 MFMA_F16_PEAK_TFLOPS = 2500.0
+METRIC = "embeddings/sec @16\u00d7150 tok; Q4_K GEMM MFMA util %; dequant/GEMV HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -106,12 +107,106 @@ def cpu_baseline(model, dims, ids, budget_s: float = 20.0) -> dict:
                       f"oracle forward (numpy float64, binary16 storage), {elapsed:.1f} s"}
 
 
+def _time_calls(torch, stream, fn, calls: int) -> tuple[float, str]:
+    """Average microseconds per call of `fn(i)` over `calls` back-to-back
+    calls, between HIP events on `stream`. The calls are captured once into a
+    HIP graph and the graph is replayed, so host launch cost does not pace the
+    GPU; if capture is refused the calls are timed as enqueued."""
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph = None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(calls):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+    except Exception as error:  # pragma: no cover - depends on the runtime
+        log(f"graph capture unavailable ({error}); timing enqueued calls")
+        graph = None
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        reps = 3 if graph is not None else 1
+        for _ in range(reps):
+            if graph is not None:
+                graph.replay()
+            else:
+                for i in range(calls):
+                    fn(i)
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / (calls * reps), ("hip graph" if graph is not None else "enqueued")
+
+
+def kernel_rates(torch, stream) -> dict:
+    """The other two parts of the metric, on the dequant-matmul of the
+    kernel benchmark (W 2048 x 2048 Q4_K, X 15 x 2048 f16, seed 1001) and on
+    the encoder's largest matrix:
+      GEMV      algorithmic bytes (W + X + Y) / time per call, over distinct
+                weight copies totalling more than the 256 MB Infinity Cache;
+      dequant   Q4_K blocks -> f16, (bytes read + bytes written) / time;
+      cpu       the same dequant-matmul by the reference's CPU check restated
+                (dequantize each row, float64 dot; oracle, one thread)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    import synth
+    from nemo_amd import _lib, runtime as rt
+    out = {}
+    for label, n, k, copies in (("q4k_gemv_15x2048x2048", 2048, 2048, 128), ("q4k_gemv_15x16384x2048", 16384, 2048, 16)):
+        m = 15
+        raw = synth.random_q4k(1001, n * k // 256)
+        weights = [rt.QuantWeight(rt.TYPE_Q4_K, n, k, raw.tobytes()) for _ in range(copies)]
+        x = torch.from_numpy(synth.normal(1008, m * k).astype(np.float16).view(np.int16).reshape(m, k)).cuda()
+        y = torch.empty((m, n), dtype=torch.int16, device="cuda")
+        us, how = _time_calls(torch, stream, lambda i: weights[i % copies].matmul(
+            x.data_ptr(), m, y.data_ptr(), _lib.MATMUL_GEMV, stream.cuda_stream), 2 * copies)
+        nbytes = n * k // 256 * 144 + 2 * m * k + 2 * m * n
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[label] = {"us_per_call": round(us, 2), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
+                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "timing": how,
+                      "weights": f"{copies} distinct copies, {copies * n * k // 256 * 144 / 1e6:.0f} MB"}
+        log(f"{label}: {us:.2f} us per call, {gbs:.0f} GB/s")
+        del weights
+    # standalone dequant of 302 MB of Q4_K blocks to f16 (16 x the 16384 x 2048 matrix)
+    nb = 16 * 16384 * 2048 // 256
+    blocks = synth.random_q4k(1001, 16384 * 2048 // 256)
+    d_raw = torch.from_numpy(np.tile(blocks, 16)).cuda()
+    d_f16 = torch.empty(nb * 256, dtype=torch.float16, device="cuda")
+    us, how = _time_calls(torch, stream, lambda i: rt.dequantize_device(rt.TYPE_Q4_K, d_raw.data_ptr(), nb * 256, 0,
+                                                                        d_f16.data_ptr(), stream.cuda_stream), 10)
+    nbytes = nb * 144 + nb * 256 * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out["q4k_dequant_f16_302MB"] = {"us_per_call": round(us, 1), "bytes_per_call": nbytes, "gbs": round(gbs, 1),
+                                    "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "timing": how}
+    log(f"dequant: {us:.1f} us per call, {gbs:.0f} GB/s")
+    del d_raw, d_f16
+    # the reference's CPU check for every element of the 15 x 2048 x 2048 product
+    raw = synth.random_q4k(1001, 2048 * 2048 // 256)
+    x16 = synth.normal(1008, 15 * 2048).astype(np.float16).reshape(15, 2048)
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < 3.0:
+        oracle.q4k_matmul_cpu(raw, x16, 15, 2048, 2048)
+        reps += 1
+    cpu_ms = (time.perf_counter() - t0) * 1e3 / reps
+    out["cpu_q4k_matmul_15x2048x2048"] = {"ms_per_call": round(cpu_ms, 2), "cores": 1, "kind": "port",
+                                          "gbs": round(2482176 / (cpu_ms * 1e-3) / 1e9, 2)}
+    log(f"cpu dequant-matmul: {cpu_ms:.1f} ms per call")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the GEMV / dequant measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the encoder pass on a single MI355X "
@@ -170,7 +265,7 @@ def main() -> int:
     all_flops = step_flops(dims)
 
     result = {
-        "metric": "embeddings/sec @16x150 tok",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "embeddings/s",
         "n_gpus": 1,
@@ -192,6 +287,9 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "gate/up Q4_K GEMM", "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
     }
+    result["q4k_gemm_mfma_util_pct"] = round(100 * achieved / MFMA_F16_PEAK_TFLOPS, 1)
+    if not args.no_kernels:
+        result["kernels"] = kernel_rates(torch, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, dims, ids)
     print(json.dumps(result), flush=True)

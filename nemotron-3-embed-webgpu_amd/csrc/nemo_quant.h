@@ -65,8 +65,9 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
 hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
                                   hipStream_t stream);
 
-// Small-M path (m <= 16): split-K wavefront GEMV with a deterministic
-// reduction through `partials` (float, at least gemv_partials_floats()).
+// Small-M path (m <= 16): MFMA GEMV, 64 rows x 2048 K per workgroup with an
+// in-workgroup reduction; K beyond 2048 splits into fp32 partials summed in
+// split order through `partials` (float, at least gemv_partials_floats()).
 size_t gemv_partials_floats(const QWeight& w, int m);
 // The GEMV's K-split count: a function of the weight's shape only.
 int gemv_splits(const QWeight& w);

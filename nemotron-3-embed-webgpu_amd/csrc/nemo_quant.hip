@@ -2,6 +2,8 @@
 // wavefront GEMV (m <= 16), GGML Q4_K / Q6_K / Q4_0 block decoding to
 // float32/f16 (bit-exact with src/gguf/quantization.ts:19-74), and the
 // fixed-order reduction of split-K partial sums.
+#include <type_traits>
+
 #include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_quant.h"
@@ -9,96 +11,175 @@
 namespace nemo {
 
 // ---------------------------------------------------------------------------
-// Split-K GEMV for m <= 16 using v_mfma_f32_16x16x32_f16: a wave owns 16
-// weight rows and one K slice; lane l works on row n0 + l%16 and the 8-column
-// slice 8*(l/16) of each 32-column MFMA step. Each lane decodes its own
-// weights straight into the B fragment (no LDS). Partials of the K slices are
-// summed in a fixed order by reduce_partials_kernel (deterministic).
+// GEMV for m <= 16 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
+// 16 T weight rows (T = 2 or 4 tiles of 16) and 8 consecutive 256-value
+// blocks of K: wave w takes block 8 * blockIdx.y + w of all T tiles. A wave
+// issues all of its loads before their first use (one memory round trip per
+// wave), each X fragment feeds the MFMAs of the T tiles, and the 8 waves'
+// sums are added in LDS in wave order (deterministic). The first T/2 tiles
+// are consecutive rows of the first half of a 128-row group and the last T/2
+// the rows 64 later, so with the gate/up rows interleaved per 128-row group
+// a workgroup holds gate and up rows of the same features and SwiGLU
+// completes in it. K beyond 2048 splits over blockIdx.y into fp32 partials
+// that the consumer sums in split order.
+//
+// MFMA operands: lane l supplies A = X[token l%16][8 consecutive k] and
+// B = W[row l%16][the same 8 k]. Lane group kq = l/16 owns four runs of 16
+// consecutive k in every block (the bytes it loads), two MFMAs per run.
 // ---------------------------------------------------------------------------
 
-constexpr int kGemvWaves = 4;
+constexpr int kGvWaves = 8;
 
-__device__ __forceinline__ void gemv_q4k_group(const QWeight& w, size_t row_bytes, int row, int k0, int kq,
-                                               const u32x4& hdr, half8v& lo, half8v& hi) {
-  const uint8_t* blk = w.blocks + (size_t)row * row_bytes + (size_t)(k0 >> 8) * 144;
-  const int g = (k0 >> 6) & 3;
-  const u32x2 q = *(const u32x2*)(blk + 16 + 32 * g + 8 * kq);
-  float dsc0, ndm0, dsc1, ndm1;
-  q4k_group_factors(hdr, g, dsc0, ndm0, dsc1, ndm1);
-  float vl[8], vh[8];
-  bytes4_fma(q.x & 0x0f0f0f0fu, dsc0, ndm0, vl);
-  bytes4_fma(q.y & 0x0f0f0f0fu, dsc0, ndm0, vl + 4);
-  bytes4_fma((q.x >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh);
-  bytes4_fma((q.y >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh + 4);
-  lo = to_half8(vl);
-  hi = to_half8(vh);
+// Q4_K: the lane group loads nibble bytes [16kq, +16) (group kq/2) and
+// [64 + 16kq, +16) (group 2 + kq/2); runs: 0 = first chunk's low nibbles,
+// 1 = its high nibbles, 2 / 3 = the same for the second chunk.
+__device__ __forceinline__ int gv_q4k_run_k(int kq, int r) {
+  return 64 * ((kq >> 1) + 2 * (r >> 1)) + 16 * (kq & 1) + 32 * (r & 1);
+}
+// Q6_K: half h = kq/2 and quadrants Qa = kq & 1 (low nibbles of ql bytes
+// [64h + 32Qa, +32)) and Qa + 2 (their high nibbles); run r: quadrant
+// Qa + 2 (r >> 1), lanes 16 (r & 1) .. +16.
+__device__ __forceinline__ int gv_q6k_run_k(int kq, int r) {
+  return 128 * (kq >> 1) + 32 * ((kq & 1) + 2 * (r >> 1)) + 16 * (r & 1);
 }
 
-__device__ __forceinline__ void gemv_q6k_group(const QWeight& w, size_t row_bytes, int row, int k0, int kq,
-                                               half8v& lo, half8v& hi) {
-  const int blk = k0 >> 8;
-  const uint8_t* rec = w.blocks + (size_t)row * row_bytes + (size_t)blk * 208;
-  const int c = (k0 >> 6) & 3, half = c >> 1, qp = c & 1;
-  const u32x2 qla = *(const u32x2*)(rec + 64 * half + 8 * kq);
-  const u32x2 qlb = *(const u32x2*)(rec + 64 * half + 32 + 8 * kq);
-  const u32x2 qh = *(const u32x2*)(rec + 128 + 32 * half + 8 * kq);
-  const int8_t* sc = (const int8_t*)(rec + 192 + 8 * half);
-  const float d = h2f(w.d[(size_t)row * (w.k >> 8) + blk]);
-  const float dsc0 = d * (float)sc[(kq >> 1) + 4 * qp];
-  const float dsc1 = d * (float)sc[(kq >> 1) + 4 * qp + 2];
-  const int s0 = 4 * qp, s1 = 4 * qp + 2;
-  float vl[8], vh[8];
-  const uint32_t la[2] = {qla.x, qla.y}, lb[2] = {qlb.x, qlb.y}, hh[2] = {qh.x, qh.y};
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t q0 = ((la[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s0) & 0x03030303u) << 4);
-    const uint32_t q1 = ((lb[i] >> s0) & 0x0f0f0f0fu) | (((hh[i] >> s1) & 0x03030303u) << 4);
-    bytes4_fma(q0, dsc0, -32.0f * dsc0, vl + 4 * i);
-    bytes4_fma(q1, dsc1, -32.0f * dsc1, vh + 4 * i);
+struct GvQ4K {
+  u32x4 hdr, qa, qb;
+  __device__ __forceinline__ void load(const QWeight& w, size_t row_bytes, int row, int blk, int kq) {
+    const uint8_t* p = w.blocks + (size_t)row * row_bytes + (size_t)blk * 144;
+    hdr = *(const u32x4*)p;
+    qa = *(const u32x4*)(p + 16 + 16 * kq);
+    qb = *(const u32x4*)(p + 80 + 16 * kq);
   }
-  lo = to_half8(vl);
-  hi = to_half8(vh);
-}
-
-template <int TYPE>
-__global__ __launch_bounds__(64 * kGemvWaves) void gemv_q_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w,
-                                                                 int M, int kchunk, float* __restrict__ partials,
-                                                                 uint16_t* __restrict__ y, int ldy) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int N = w.n;
-  const int n0 = (blockIdx.x * kGemvWaves + wave) * 16;
-  if (n0 >= N) return;
-  const int kbeg = blockIdx.y * kchunk, kend = min(w.k, kbeg + kchunk);
-  const int c = lane & 15, kq = lane >> 4;
-  const int row = min(n0 + c, N - 1);
-  const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
-  const uint16_t* xr = x + (size_t)min(c, M - 1) * ldx + 8 * kq;
-  float4v acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = kbeg; kb < kend; kb += 256) {
-    u32x4 hdr;
-    if constexpr (TYPE == kQ4_K) hdr = *(const u32x4*)(w.blocks + (size_t)row * row_bytes + (size_t)(kb >> 8) * 144);
+  // The 16 values of run r as two f16 fragments (k order).
+  __device__ __forceinline__ void run(int kq, int r, half8v& f0, half8v& f1) const {
+    float dsc0, ndm0, dsc1, ndm1;
+    q4k_group_factors(hdr, (kq >> 1) + 2 * (r >> 1), dsc0, ndm0, dsc1, ndm1);
+    const u32x4 q = (r >> 1) ? qb : qa;
+    const int sh = 4 * (r & 1);
+    const float dsc = (r & 1) ? dsc1 : dsc0, ndm = (r & 1) ? ndm1 : ndm0;
+    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+    float v[16];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int k0 = kb + 64 * g;
-      half8v blo, bhi;
-      if constexpr (TYPE == kQ4_K) gemv_q4k_group(w, row_bytes, row, k0, kq, hdr, blo, bhi);
-      else gemv_q6k_group(w, row_bytes, row, k0, kq, blo, bhi);
-      const half8v alo = *(const half8v*)(xr + k0);
-      const half8v ahi = *(const half8v*)(xr + k0 + 32);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, blo, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bhi, acc, 0, 0, 0);
+    for (int i = 0; i < 4; ++i) bytes4_fma(opaque((words[i] >> sh) & 0x0f0f0f0fu), dsc, ndm, v + 4 * i);
+    f0 = to_half8(v);
+    f1 = to_half8(v + 8);
+  }
+};
+
+struct GvQ6K {
+  u32x4 ql0, ql1, qh0, qh1, sc;
+  uint16_t d;
+  __device__ __forceinline__ void load(const QWeight& w, size_t row_bytes, int row, int blk, int kq) {
+    const uint8_t* rec = w.blocks + (size_t)row * row_bytes + (size_t)blk * 208;
+    const int h = kq >> 1, qa = kq & 1;
+    ql0 = *(const u32x4*)(rec + 64 * h + 32 * qa);
+    ql1 = *(const u32x4*)(rec + 64 * h + 32 * qa + 16);
+    qh0 = *(const u32x4*)(rec + 128 + 32 * h);
+    qh1 = *(const u32x4*)(rec + 128 + 32 * h + 16);
+    sc = *(const u32x4*)(rec + 192);
+    d = w.d[(size_t)row * (w.k >> 8) + blk];
+  }
+  __device__ __forceinline__ void run(int kq, int r, half8v& f0, half8v& f1) const {
+    const int h = kq >> 1, Q = (kq & 1) + 2 * (r >> 1), jh = r & 1;
+    const u32x4 ql = jh ? ql1 : ql0, qh = jh ? qh1 : qh0;
+    // scale of (half h, lanes 16 jh.., quadrant Q) is scales[8h + jh + 2Q]
+    const int sb = 8 * h + jh + 2 * Q;
+    const uint32_t sw = sb < 4 ? sc.x : sb < 8 ? sc.y : sb < 12 ? sc.z : sc.w;
+    const float dsc = h2f(d) * (float)(int8_t)((sw >> (8 * (sb & 3))) & 0xffu);
+    const int ls = 4 * (r >> 1), hs = 2 * Q;
+    const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = ((lw[i] >> ls) & 0x0f0f0f0fu) | (((hw[i] >> hs) & 0x03030303u) << 4);
+      bytes4_fma(opaque(q), dsc, -32.0f * dsc, v + 4 * i);
     }
+    f0 = to_half8(v);
+    f1 = to_half8(v + 8);
   }
-  // D layout of a 16x16 MFMA block: lane l, register i -> row 4*(l/16) + i,
-  // column l%16.
-  const int col = n0 + c;
-  if (col >= N) return;
+};
+
+enum GvMode { kGvStore = 0, kGvPartial = 1, kGvSwiGLU = 2 };
+
+template <int TYPE, int MODE, int kGvTiles>
+__global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w, int M,
+                                                             void* __restrict__ out, int ldo) {
+  using Raw = typename std::conditional<TYPE == kQ4_K, GvQ4K, GvQ6K>::type;
+  // P 16-row tiles of gate-half rows and the P matching tiles 64 rows later;
+  // 4 / P workgroups per 128-row group.
+  constexpr int P = kGvTiles / 2, G = 4 / P;
+  __shared__ float4v red[kGvWaves][kGvTiles][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kq = lane >> 4, c = lane & 15;
+  const int N = w.n, nblocks = w.k >> 8;
+  const int n0 = 128 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G);
+  const int blk = kGvWaves * blockIdx.y + wave;
+  const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
+
+  float4v acc[kGvTiles];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = 4 * kq + i;
-    if (m >= M) continue;
-    if (partials == nullptr) y[(size_t)m * ldy + col] = f2h(acc[i]);
-    else partials[((size_t)blockIdx.y * M + m) * N + col] = acc[i];
+  for (int t = 0; t < kGvTiles; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
+  if (blk < nblocks) {
+    Raw raw[kGvTiles];
+#pragma unroll
+    for (int t = 0; t < kGvTiles; ++t) raw[t].load(w, row_bytes, min(n0 + 16 * (t % P) + 64 * (t / P) + c, N - 1), blk, kq);
+    const uint16_t* xr = x + (size_t)min(c, M - 1) * ldx + 256 * blk;
+    half8v xa[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : gv_q6k_run_k(kq, r);
+      xa[2 * r] = *(const half8v*)(xr + k);
+      xa[2 * r + 1] = *(const half8v*)(xr + k + 8);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int t = 0; t < kGvTiles; ++t) {
+        half8v f0, f1;
+        raw[t].run(kq, r, f0, f1);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r], f0, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r + 1], f1, acc[t], 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < kGvTiles; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+
+  // D layout: lane l, register i -> token 4 (l / 16) + i, row l % 16 of the tile.
+  auto tile_sum = [&](int t) {
+    float4v s = red[0][t][lane];
+#pragma unroll
+    for (int v = 1; v < kGvWaves; ++v) s += red[v][t][lane];
+    return s;
+  };
+  if constexpr (MODE == kGvSwiGLU) {
+    if (wave >= P) return;
+    const float4v g = tile_sum(wave), u = tile_sum(wave + P);
+    const int f = 64 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G) + 16 * wave + c;
+    if (n0 + 16 * wave + c + 64 >= N) return;
+    uint16_t* y = (uint16_t*)out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kq + i;
+      if (m >= M) continue;
+      const float gv = (float)(half_t)g[i], uv = (float)(half_t)u[i];
+      y[(size_t)m * ldo + f] = f2h(gv / (1.0f + expf(-gv)) * uv);
+    }
+  } else {
+    if (wave >= kGvTiles) return;
+    const float4v s = tile_sum(wave);
+    const int row = n0 + 16 * (wave % P) + 64 * (wave / P) + c;
+    if (row >= N) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kq + i;
+      if (m >= M) continue;
+      if constexpr (MODE == kGvStore)
+        ((uint16_t*)out)[(size_t)m * ldo + row] = f2h(s[i]);
+      else
+        ((float*)out)[((size_t)blockIdx.y * M + m) * N + row] = s[i];
+    }
   }
 }
 
@@ -143,12 +224,8 @@ __global__ void reduce_swiglu_kernel(const float* __restrict__ partials, int spl
 }
 
 int gemv_splits(const QWeight& w) {
-  // Enough waves to keep every SIMD streaming: target >= 4096 waves.
-  const int col_waves = (w.n + 15) / 16;
-  const int blocks = w.k / 256;
-  int splits = 1;
-  while (splits < blocks && col_waves * splits < 4096 && blocks % (splits * 2) == 0) splits *= 2;
-  return splits;
+  // One workgroup row covers 8 blocks (2048 values) of K.
+  return ((w.k >> 8) + kGvWaves - 1) / kGvWaves;
 }
 
 size_t gemv_partials_floats(const QWeight& w, int m) {
@@ -156,47 +233,58 @@ size_t gemv_partials_floats(const QWeight& w, int m) {
   return s > 1 ? (size_t)s * m * w.n : 0;
 }
 
-hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, float* partials,
-                       hipStream_t stream) {
-  if (m <= 0) return hipSuccess;
-  if (m > 16) return hipErrorInvalidValue;
-  const int splits = gemv_splits(w);
-  const int kchunk = w.k / splits;
-  if (splits > 1 && partials == nullptr) return hipErrorInvalidValue;
-  dim3 grid((w.n + 16 * kGemvWaves - 1) / (16 * kGemvWaves), splits);
-  float* p = splits > 1 ? partials : nullptr;
-  if (w.type == kQ4_K)
-    gemv_q_kernel<kQ4_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, y, ldy);
-  else if (w.type == kQ6_K)
-    gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, y, ldy);
-  else
-    return hipErrorInvalidValue;
-  if (splits > 1) return launch_reduce_partials(partials, splits, m, w.n, y, ldy, stream);
-  return hipGetLastError();
+template <int TYPE, int MODE>
+static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
+                               hipStream_t stream) {
+  // 4 tiles per wave (X fragments reused 4 times) once that alone gives
+  // every CU a workgroup; else 2, which halves each wave's serial decode. A
+  // row's arithmetic is the same either way.
+  const int groups = (w.n + 127) / 128;
+  if (2 * groups * gemv_splits(w) < 256) {
+    dim3 grid(4 * ((w.n + 127) / 128), gemv_splits(w));
+    gemv_kernel<TYPE, MODE, 2><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  } else {
+    dim3 grid(2 * ((w.n + 127) / 128), gemv_splits(w));
+    gemv_kernel<TYPE, MODE, 4><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  }
+}
+
+template <int MODE>
+static void launch_gemv_typed(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
+                              hipStream_t stream) {
+  if (w.type == kQ4_K) launch_gemv_kernel<kQ4_K, MODE>(x, ldx, w, m, out, ldo, stream);
+  else launch_gemv_kernel<kQ6_K, MODE>(x, ldx, w, m, out, ldo, stream);
 }
 
 hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, void* out, int ldo,
                           float* partials, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
   if (m > 16 || (w.type != kQ4_K && w.type != kQ6_K)) return hipErrorInvalidValue;
-  if (epilogue == kEpiStore) return launch_gemv(x, ldx, w, (uint16_t*)out, ldo, m, partials, stream);
-  const int splits = gemv_splits(w);
-  const int kchunk = w.k / splits;
-  dim3 grid((w.n + 16 * kGemvWaves - 1) / (16 * kGemvWaves), splits);
-  // kEpiPartial: the caller's buffer receives [splits][m][n] fp32 sums;
-  // kEpiSwiGLU: sums go to `partials`, then the SwiGLU reduction.
-  float* p = epilogue == kEpiPartial ? (float*)out : partials;
-  if (p == nullptr || (epilogue == kEpiPartial && ldo != w.n)) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
-  if (w.type == kQ4_K)
-    gemv_q_kernel<kQ4_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, nullptr, 0);
-  else
-    gemv_q_kernel<kQ6_K><<<grid, 64 * kGemvWaves, 0, stream>>>(x, ldx, w, m, kchunk, p, nullptr, 0);
-  if (epilogue == kEpiSwiGLU) {
-    const int64_t total = (int64_t)m * (w.n / 2);
-    reduce_swiglu_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(p, splits, m, w.n, (uint16_t*)out, ldo);
+  const int splits = gemv_splits(w);
+  if (epilogue == kEpiPartial) {
+    // [splits][m][n] fp32 sums into `out` (row stride n)
+    if (ldo != w.n || out == nullptr) return hipErrorInvalidValue;
+    launch_gemv_typed<kGvPartial>(x, ldx, w, m, out, ldo, stream);
+    return hipGetLastError();
   }
+  if (splits == 1) {
+    if (epilogue == kEpiStore) launch_gemv_typed<kGvStore>(x, ldx, w, m, out, ldo, stream);
+    else launch_gemv_typed<kGvSwiGLU>(x, ldx, w, m, out, ldo, stream);
+    return hipGetLastError();
+  }
+  if (partials == nullptr) return hipErrorInvalidValue;
+  launch_gemv_typed<kGvPartial>(x, ldx, w, m, partials, w.n, stream);
+  if (epilogue == kEpiStore) return launch_reduce_partials(partials, splits, m, w.n, (uint16_t*)out, ldo, stream);
+  const int64_t total = (int64_t)m * (w.n / 2);
+  reduce_swiglu_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(partials, splits, m, w.n, (uint16_t*)out,
+                                                                            ldo);
   return hipGetLastError();
+}
+
+hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, float* partials,
+                       hipStream_t stream) {
+  return launch_gemv_ex(x, ldx, w, m, kEpiStore, y, ldy, partials, stream);
 }
 
 // ---------------------------------------------------------------------------
