@@ -319,12 +319,11 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(const uint16_t* __restric
 // ---------------------------------------------------------------------------
 // Two-pass path for large batches. A bandwidth-bound pre-pass expands W to an
 // f16 [n][k] matrix with the same decoders the fused kernels use (identical
-// f16 values), then gemm_f16_kernel runs 256 x 256 x 64 tiles with both
-// operands copied global -> LDS by global_load_lds_dwordx4 into the swizzled
-// layout described above, 8 waves of 64 x 128. Each wave issues the same MFMA
-// sequence per output element as the fused kernels (16-column steps in K
-// order), so the two paths give bit-identical results.
-// LDS: 2 x 32 KB (X) + 2 x 32 KB (W) = 128 KB, dynamic.
+// f16 values), then gemm_f16_kernel runs 256 x BN x 64 tiles (BN 256 or 128)
+// with both operands copied global -> LDS by global_load_lds_dwordx4 into the
+// swizzled layout described above, 4 x BN/128 waves of 64 x 128. Each wave
+// issues the same MFMA sequence per output element as the fused kernels
+// (16-column steps in K order), so the two paths give bit-identical results.
 // ---------------------------------------------------------------------------
 
 template <int TYPE>
@@ -346,41 +345,52 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
   *(half8v*)(dst + 40) = hi[1];
 }
 
-constexpr int kF16Lds = 4 * kBigXStage;
+// LDS of the f16 GEMM: two stages of the 256 x 64 X tile and the BN x 64 W
+// tile (128 bytes per row): 128 KB for BN 256, 96 KB for BN 128.
+constexpr int f16_lds_bytes(int bn) { return 2 * kBigXStage + 2 * bn * 128; }
 
-template <int EPI>
-__global__ __launch_bounds__(512) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
-                                                       const uint16_t* __restrict__ wt, int N, int K, int M,
-                                                       int kchunk, void* __restrict__ out, int ldo) {
+template <int EPI, int BN>
+__global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                                    const uint16_t* __restrict__ wt, int N, int K,
+                                                                    int M, int kchunk, void* __restrict__ out,
+                                                                    int ldo) {
+  // 4 waves along M (64 rows each) x BN/128 along N (128 columns each).
+  constexpr int WAVES = 4 * BN / 128, MI = 2;
+  constexpr int XI = 256 / 8 / WAVES, WI = BN / 8 / WAVES;  // copy instructions per wave and stage
+  constexpr int WSTAGE = BN * 128;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* sX = smem;                   // [2][256 rows][128 B]
-  uint8_t* sW = smem + 2 * kBigXStage;  // [2][256 rows][128 B]
-  constexpr int MI = 2;
+  uint8_t* sW = smem + 2 * kBigXStage;  // [2][BN rows][128 B]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 3, wn = wave >> 2;
-  const int m0 = blockIdx.y * kBigBM, n0 = blockIdx.x * kBigBN;
+  const int m0 = blockIdx.y * kBigBM, n0 = blockIdx.x * BN;
   const int kbeg = blockIdx.z * kchunk;
   const int nsteps = kchunk / kBK;
 
-  // Wave w copies rows [32w, 32w + 32) of both tiles, 8 rows per instruction;
-  // lane l -> row R + l/8, slot l%8 holding logical chunk (l%8) ^ f(row).
-  const uint16_t* xsrc[4];
-  const uint16_t* wsrc[4];
+  // Each copy instruction moves 8 whole rows: lane l -> row R + l/8, slot
+  // l%8 holding logical chunk (l%8) ^ f(row). Wave w copies X rows
+  // [8 XI w, +8 XI) and W rows [8 WI w, +8 WI).
+  const uint16_t* xsrc[XI];
+  const uint16_t* wsrc[WI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 32 * wave + 8 * i + (lane >> 3);
-    const int c = (lane & 7) ^ xswz(r);
-    xsrc[i] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * c;
-    wsrc[i] = wt + (size_t)min(n0 + r, N - 1) * K + 8 * c;
+  for (int i = 0; i < XI; ++i) {
+    const int r = 8 * XI * wave + 8 * i + (lane >> 3);
+    xsrc[i] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * ((lane & 7) ^ xswz(r));
+  }
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int r = 8 * WI * wave + 8 * i + (lane >> 3);
+    wsrc[i] = wt + (size_t)min(n0 + r, N - 1) * K + 8 * ((lane & 7) ^ xswz(r));
   }
   auto copy = [&](int stage, int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XI; ++i)
       __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + k0),
-                                       (lds_void*)(sX + stage * kBigXStage + (32 * wave + 8 * i) * 128), 16, 0, 0);
+                                       (lds_void*)(sX + stage * kBigXStage + (8 * XI * wave + 8 * i) * 128), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
       __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + k0),
-                                       (lds_void*)(sW + stage * kBigXStage + (32 * wave + 8 * i) * 128), 16, 0, 0);
-    }
+                                       (lds_void*)(sW + stage * WSTAGE + (8 * WI * wave + 8 * i) * 128), 16, 0, 0);
   };
 
   float16v acc[MI][4];
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(512) void gemm_f16_kernel(const uint16_t* __restric
 
   auto mfma_step = [&](int stage) {
     const uint8_t* xs = sX + stage * kBigXStage;
-    const uint8_t* ws = sW + stage * kBigXStage;
+    const uint8_t* ws = sW + stage * WSTAGE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int c = 2 * ks + (lane >> 5);
@@ -417,11 +427,12 @@ __global__ __launch_bounds__(512) void gemm_f16_kernel(const uint16_t* __restric
 
   // The copies of step s+2 are issued right after the barrier that frees
   // their stage and have the whole of step s+1 to land. Loads complete in
-  // order: vmcnt(8) leaves the 8 copies of the newer stage in flight.
+  // order: vmcnt(XI + WI) leaves the newer stage's copies in flight.
   auto kat = [&](int s) { return kbeg + min(s, nsteps - 1) * kBK; };
   copy(0, kat(0));
   copy(1, kat(1));
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  if constexpr (XI + WI == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
   __syncthreads();
   for (int s = 0; s < nsteps; s += 2) {
     mfma_step(0);
@@ -482,32 +493,49 @@ static int gemm_variant(const QWeight& w, int m, int splits) {
   return (m >= 512 && ((m + 255) / 256) * ntiles * splits >= 512) ? kVarLds256 : kVarLds128;
 }
 
-bool gemm_two_pass(const QWeight& w, int m, int splits) {
-  // The f16 GEMM runs 256 x 256 tiles: worth the expansion pass once the
-  // tiles alone give every CU a workgroup.
-  return w.n % kBigBN == 0 && ((m + kBigBM - 1) / kBigBM) * (w.n / kBigBN) * splits >= 256;
+// Tile width of the two-pass GEMM for this problem, or 0 when the fused
+// kernels are the better choice (measured on the encoder's shapes): 256-column
+// tiles once they alone give every CU a workgroup; 128-column tiles for
+// unsplit problems with at least 64 of them (the QKV projection). Split-K
+// problems with fewer 256-column tiles do better on the fused 128-row tiles,
+// of which two or more fit on a CU.
+static int two_pass_bn(const QWeight& w, int m, int splits) {
+  const int mt = (m + kBigBM - 1) / kBigBM;
+  if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= 256) return 256;
+  if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) return 128;
+  return 0;
+}
+
+bool gemm_two_pass(const QWeight& w, int m, int splits) { return two_pass_bn(w, m, splits) != 0; }
+
+template <int BN>
+static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, const uint16_t* wexp, const QWeight& w,
+                       int m, int kchunk, void* out, int ldo, hipStream_t stream) {
+  constexpr int lds = f16_lds_bytes(BN);
+  auto launch = [&](auto kernel) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+      (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      configured = true;
+    }
+    kernel<<<grid, 4 * BN / 128 * 64, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
+  };
+  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN>);
+  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN>);
+  else launch(gemm_f16_kernel<kEpiSwiGLU, BN>);
 }
 
 static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
-                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream) {
-  if (epilogue == kEpiSwiGLU && w.n % kBigBN) return hipErrorInvalidValue;
+                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream, int bn) {
+  if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (w.type == kQ4_K) expand_kernel<kQ4_K><<<blocks, 256, 0, stream>>>(w, wexp);
   else expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
   const int kchunk = w.k / splits;
-  dim3 grid((w.n + kBigBN - 1) / kBigBN, (m + kBigBM - 1) / kBigBM, splits);
-  auto launch = [&](auto kernel) {
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-      (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kF16Lds);
-      configured = true;
-    }
-    kernel<<<grid, 512, kF16Lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
-  };
-  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore>);
-  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial>);
-  else launch(gemm_f16_kernel<kEpiSwiGLU>);
+  dim3 grid((w.n + bn - 1) / bn, (m + kBigBM - 1) / kBigBM, splits);
+  if (bn == 256) launch_f16<256>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream);
+  else launch_f16<128>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream);
   return hipGetLastError();
 }
 
@@ -519,7 +547,8 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
   if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
-  if (wexp && gemm_two_pass(w, m, splits)) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream);
+  const int bn = wexp ? two_pass_bn(w, m, splits) : 0;
+  if (bn) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, bn);
   const int var = gemm_variant(w, m, splits);
 #define NEMO_LAUNCH(T)                                                                                              \
   if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
@@ -542,7 +571,8 @@ hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, in
                                 uint16_t* wexp, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
   if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
-  return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream);
+  const int bn = w.n % 256 == 0 ? 256 : 128;
+  return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream, bn);
 }
 
 }  // namespace nemo
