@@ -107,6 +107,20 @@ def cpu_baseline(model, dims, ids, budget_s: float = 20.0) -> dict:
                       f"oracle forward (numpy float64, binary16 storage), {elapsed:.1f} s"}
 
 
+def committed_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", "gate_up_traffic_16x150.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def _time_calls(torch, stream, fn, calls: int) -> tuple[float, str]:
     """Average microseconds per call of `fn(i)` over `calls` back-to-back
     calls, between HIP events on `stream`. The calls are captured once into a
@@ -284,8 +298,10 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "projection_tflops": round(all_flops / (ms * 1e-3) / 1e12, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "gate/up Q4_K GEMM", "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
+                     "kernel": "gate/up Q4_K dequant-matmul (expand + f16 MFMA GEMM, SwiGLU epilogue)",
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 2),
+                     "traffic_source": "profiles/gate_up_traffic_16x150.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)"},
     }
     result["q4k_gemm_mfma_util_pct"] = round(100 * achieved / MFMA_F16_PEAK_TFLOPS, 1)
     if not args.no_kernels:
