@@ -37,6 +37,11 @@ typedef int32_t nemo_status;
 #define NEMO_TYPE_Q4_0 2
 #define NEMO_TYPE_Q4_K 12
 #define NEMO_TYPE_Q6_K 14
+/* Q4_0 in the wgpack "q4_0-tile32-compact" layout: 20-byte records
+ * [f16 d][2 zero bytes][16 nibble bytes] ordered tile (32 rows) -> 32-value
+ * block -> row (src/prepacked/format.ts:65-99). Not a GGML type code; the
+ * tensor is held and returned as NEMO_TYPE_Q4_0. */
+#define NEMO_TYPE_Q4_0_TILE32 258
 
 typedef struct nemo_ctx nemo_ctx;
 typedef struct nemo_model nemo_model;
@@ -82,8 +87,10 @@ nemo_status nemo_model_create(nemo_ctx* ctx, const nemo_dims* dims, nemo_model**
 
 /* Upload one tensor (replaces createBufferWithData per tensor,
  * src/webgpu/model.ts:264-266,283-286). `dims` are GGUF dims (ne0 first: a
- * matrix of n rows by k columns is {k, n}). Matrices: NEMO_TYPE_Q4_K or
- * NEMO_TYPE_Q6_K raw GGUF blocks; norms: NEMO_TYPE_F32; token_embd.weight:
+ * matrix of n rows by k columns is {k, n}). Matrices: NEMO_TYPE_Q4_K,
+ * NEMO_TYPE_Q6_K or NEMO_TYPE_Q4_0 raw GGUF blocks, or NEMO_TYPE_Q4_0_TILE32
+ * records of a .wgpack (k a multiple of 256 for every matrix type); norms:
+ * NEMO_TYPE_F32; token_embd.weight:
  * NEMO_TYPE_Q6_K or NEMO_TYPE_F16. Names are the GGUF names; the fused
  * blk.N.attn_qkv.weight / blk.N.ffn_gate_up.weight may be given directly or
  * as their parts (attn_q/attn_k/attn_v, ffn_gate/ffn_up), fused at finalize
@@ -151,7 +158,8 @@ nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, 
 
 /* Upload one quantized matrix of n rows by k columns (k % 256 == 0) from raw
  * GGUF bytes: QuantMatmulKernel.createRun's weight buffer
- * (src/webgpu/quant-matmul.ts:503-509). Types Q4_K and Q6_K. */
+ * (src/webgpu/quant-matmul.ts:503-509). Types Q4_K, Q6_K, Q4_0 (GGUF blocks) and
+ * NEMO_TYPE_Q4_0_TILE32 (the wgpack records; quant-matmul.ts:99-108). */
 nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int32_t k, const void* bytes,
                                size_t n_bytes, nemo_weight** out);
 nemo_status nemo_weight_destroy(nemo_weight* weight);

@@ -74,7 +74,7 @@ struct DevTensor {
   int type = -1;
   std::vector<int64_t> dims;
   DevPtr data;   // raw bytes (Q6_K: 208-byte records)
-  DevPtr d6;     // Q6_K matrices: per-block f16 scale (null when stored raw)
+  DevPtr d6;     // Q6_K / Q4_0 matrices: per-block f16 scale (null when stored raw)
   size_t bytes = 0;  // GGUF byte size
   // Gate/up rows reordered per 128-row tile (64 gate rows, then the matching
   // 64 up rows) for the GEMM's SwiGLU epilogue.
@@ -94,14 +94,14 @@ void interleave_rows(DevPtr& buf, size_t row_bytes, int64_t F) {
   buf = std::move(out);
 }
 
+// Bytes per row of a split matrix's scale array (Q6_K: one f16 per 256
+// values; Q4_0: one per 32).
+size_t scale_row_bytes(int type, int64_t k) { return type == kQ4_0 ? (size_t)(k / 32) * 2 : (size_t)(k / 256) * 2; }
+
 void interleave_gate_up(DevTensor& t, int64_t F) {
   const int k = (int)t.dims[0];
-  if (t.type == kQ4_K) {
-    interleave_rows(t.data, (size_t)(k / 256) * 144, F);
-  } else {
-    interleave_rows(t.data, (size_t)(k / 256) * 208, F);
-    interleave_rows(t.d6, (size_t)(k / 256) * 2, F);
-  }
+  interleave_rows(t.data, qweight_row_bytes(t.type, k), F);
+  if (t.d6) interleave_rows(t.d6, scale_row_bytes(t.type, k), F);
 }
 
 size_t ggml_bytes(int type, const std::vector<int64_t>& dims) {
@@ -120,8 +120,37 @@ size_t ggml_bytes(int type, const std::vector<int64_t>& dims) {
     case kQ6_K:
       if (dims[0] % 256) fail(NEMO_ERR_INVALID, "K-quant row length must be a multiple of 256");
       return (size_t)(n / 256) * (type == kQ4_K ? 144 : 210);
+    case NEMO_TYPE_Q4_0_TILE32:
+      if (dims.size() != 2 || dims[0] % 32) fail(NEMO_ERR_INVALID, "compact Q4_0 needs [k, n] with k a multiple of 32");
+      return (size_t)((dims[1] + 31) / 32) * (size_t)(dims[0] / 32) * 32 * 20;
     default: fail(NEMO_ERR_UNSUPPORTED, "unsupported GGML type " + std::to_string(type));
   }
+}
+
+// GGUF Q4_0 blocks (18 bytes: f16 d, 16 nibble bytes), row major, to the
+// split layout (see QWeight).
+void split_q40(const uint8_t* raw, int64_t nb, std::vector<uint8_t>& nib, std::vector<uint16_t>& d) {
+  nib.resize((size_t)nb * 16);
+  d.resize((size_t)nb);
+  for (int64_t b = 0; b < nb; ++b) {
+    d[b] = (uint16_t)(raw[b * 18] | (raw[b * 18 + 1] << 8));
+    memcpy(nib.data() + b * 16, raw + b * 18 + 2, 16);
+  }
+}
+
+// wgpack tile32-compact records (src/prepacked/format.ts:65-99): record of
+// row r, 32-value block kb sits at ((r / 32) * kBlocks + kb) * 32 + r % 32,
+// 20 bytes [f16 d][2 zero bytes][16 nibble bytes]; to the split layout.
+void split_q40_tile32(const uint8_t* rec, int64_t k, int64_t n, std::vector<uint8_t>& nib, std::vector<uint16_t>& d) {
+  const int64_t kb_count = k / 32;
+  nib.resize((size_t)(n * kb_count) * 16);
+  d.resize((size_t)(n * kb_count));
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t kb = 0; kb < kb_count; ++kb) {
+      const uint8_t* src = rec + (((r / 32) * kb_count + kb) * 32 + r % 32) * 20;
+      d[r * kb_count + kb] = (uint16_t)(src[0] | (src[1] << 8));
+      memcpy(nib.data() + (r * kb_count + kb) * 16, src + 4, 16);
+    }
 }
 
 // Split raw Q6_K blocks into 208-byte records + f16 scales (see QWeight).
@@ -139,20 +168,33 @@ void upload_tensor(DevTensor& t, int type, const std::vector<int64_t>& dims, con
   const size_t expect = ggml_bytes(type, dims);
   if (n_bytes != expect)
     fail(NEMO_ERR_INVALID, name + " has " + std::to_string(n_bytes) + " bytes; expected " + std::to_string(expect));
-  t.type = type;
   t.dims = dims;
-  t.bytes = n_bytes;
-  // Q6_K matrices are split for aligned GEMM loads; the Q6_K token table
-  // stays in its raw 210-byte rows (read by the embedding lookup).
-  if (type == kQ6_K && name != "token_embd.weight") {
-    std::vector<uint8_t> rec;
-    std::vector<uint16_t> d;
-    const int64_t nb = (int64_t)(n_bytes / 210);
-    split_q6k((const uint8_t*)bytes, nb, rec, d);
-    t.data = dev_alloc(rec.size(), "Q6_K records");
-    t.d6 = dev_alloc(d.size() * 2, "Q6_K scales");
+  auto put = [&](const std::vector<uint8_t>& rec, const std::vector<uint16_t>& d, const char* what) {
+    t.data = dev_alloc(rec.size(), what);
+    t.d6 = dev_alloc(d.size() * 2, "block scales");
     hip_check(hipMemcpy(t.data.get(), rec.data(), rec.size(), hipMemcpyHostToDevice), "upload");
     hip_check(hipMemcpy(t.d6.get(), d.data(), d.size() * 2, hipMemcpyHostToDevice), "upload");
+  };
+  // Q6_K and Q4_0 matrices are split for aligned GEMM loads; the Q6_K token
+  // table stays in its raw 210-byte rows (read by the embedding lookup).
+  const bool matrix = dims.size() == 2 && name != "token_embd.weight";
+  std::vector<uint8_t> rec;
+  std::vector<uint16_t> d;
+  if (type == NEMO_TYPE_Q4_0_TILE32) {
+    split_q40_tile32((const uint8_t*)bytes, dims[0], dims[1], rec, d);
+    put(rec, d, "Q4_0 nibbles");
+    t.type = kQ4_0;
+    t.bytes = (size_t)(dims[0] / 32) * dims[1] * 18;  // GGUF size, as get_tensor returns it
+    return;
+  }
+  t.type = type;
+  t.bytes = n_bytes;
+  if (type == kQ6_K && matrix) {
+    split_q6k((const uint8_t*)bytes, (int64_t)(n_bytes / 210), rec, d);
+    put(rec, d, "Q6_K records");
+  } else if (type == kQ4_0 && matrix) {
+    split_q40((const uint8_t*)bytes, (int64_t)(n_bytes / 18), rec, d);
+    put(rec, d, "Q4_0 nibbles");
   } else {
     t.data = dev_alloc(n_bytes, name.c_str());
     hip_check(hipMemcpy(t.data.get(), bytes, n_bytes, hipMemcpyHostToDevice), "upload");
@@ -402,7 +444,7 @@ static void fuse_rows(nemo_model* m, const std::string& name, const std::vector<
   const DevTensor& first = *src[0];
   int64_t rows = 0;
   for (auto* t : src) {
-    if (t->type != first.type || (t->type != kQ4_K && t->type != kQ6_K) || t->dims.size() != 2 ||
+    if (t->type != first.type || (t->type != kQ4_K && t->type != kQ6_K && t->type != kQ4_0) || t->dims.size() != 2 ||
         t->dims[0] != first.dims[0]) {
       std::string all;
       for (const auto& p : parts) all += (all.empty() ? "" : ", ") + p;
@@ -416,14 +458,16 @@ static void fuse_rows(nemo_model* m, const std::string& name, const std::vector<
   f.bytes = ggml_bytes(f.type, f.dims);
   const size_t row_bytes = qweight_row_bytes(f.type, (int)first.dims[0]);
   f.data = dev_alloc(row_bytes * rows, "fused matrix");
-  if (f.type == kQ6_K) f.d6 = dev_alloc((size_t)(first.dims[0] / 256) * rows * 2, "fused scales");
+  const bool split = first.d6 != nullptr;
+  const size_t drow = scale_row_bytes(f.type, first.dims[0]);
+  if (split) f.d6 = dev_alloc(drow * rows, "fused scales");
   size_t off = 0, doff = 0;
   for (auto* t : src) {
     const size_t bytes = row_bytes * t->dims[1];
     hip_check(hipMemcpy((uint8_t*)f.data.get() + off, t->data.get(), bytes, hipMemcpyDeviceToDevice), "fuse");
     off += bytes;
-    if (f.type == kQ6_K) {
-      const size_t db = (size_t)(first.dims[0] / 256) * t->dims[1] * 2;
+    if (split) {
+      const size_t db = drow * t->dims[1];
       hip_check(hipMemcpy((uint8_t*)f.d6.get() + doff, t->d6.get(), db, hipMemcpyDeviceToDevice), "fuse");
       doff += db;
     }
@@ -435,7 +479,7 @@ static void fuse_rows(nemo_model* m, const std::string& name, const std::vector<
 static QWeight matrix(nemo_model* m, const std::string& name, int64_t k, int64_t n) {
   const DevTensor& t = need(m, name);
   if (t.dims.size() != 2) fail(NEMO_ERR_INVALID, "invalid matrix " + name);
-  if (t.type != kQ4_K && t.type != kQ6_K)
+  if (t.type != kQ4_K && t.type != kQ6_K && t.type != kQ4_0)
     fail(NEMO_ERR_UNSUPPORTED, "unsupported matrix type " + std::to_string(t.type) + " for " + name);
   if (t.dims[0] != k || t.dims[1] != n)
     fail(NEMO_ERR_INVALID, name + " has dims [" + std::to_string(t.dims[0]) + ", " + std::to_string(t.dims[1]) +
@@ -514,6 +558,18 @@ nemo_status nemo_model_get_tensor(nemo_model* model, const char* name, int32_t* 
         memcpy(o + b * 210, rec.data() + b * 208, 208);
         o[b * 210 + 208] = (uint8_t)(dd[b] & 0xff);
         o[b * 210 + 209] = (uint8_t)(dd[b] >> 8);
+      }
+    } else if (t.type == kQ4_0 && t.d6) {
+      const int64_t nb = (int64_t)(t.bytes / 18);
+      std::vector<uint8_t> nib((size_t)nb * 16);
+      std::vector<uint16_t> dd((size_t)nb);
+      hip_check(hipMemcpy(nib.data(), t.data.get(), nib.size(), hipMemcpyDeviceToHost), "download");
+      hip_check(hipMemcpy(dd.data(), t.d6.get(), dd.size() * 2, hipMemcpyDeviceToHost), "download");
+      uint8_t* o = (uint8_t*)out;
+      for (int64_t b = 0; b < nb; ++b) {
+        o[b * 18] = (uint8_t)(dd[b] & 0xff);
+        o[b * 18 + 1] = (uint8_t)(dd[b] >> 8);
+        memcpy(o + b * 18 + 2, nib.data() + b * 16, 16);
       }
     } else {
       hip_check(hipMemcpy(out, t.data.get(), t.bytes, hipMemcpyDeviceToHost), "download");
@@ -887,7 +943,8 @@ nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int3
                                size_t n_bytes, nemo_weight** out) {
   return guarded([&] {
     if (!ctx || !out || !bytes) fail(NEMO_ERR_INVALID, "null argument");
-    if (ggml_type != kQ4_K && ggml_type != kQ6_K) fail(NEMO_ERR_UNSUPPORTED, "weight type must be Q4_K or Q6_K");
+    if (ggml_type != kQ4_K && ggml_type != kQ6_K && ggml_type != kQ4_0 && ggml_type != NEMO_TYPE_Q4_0_TILE32)
+      fail(NEMO_ERR_UNSUPPORTED, "weight type must be Q4_K, Q6_K, Q4_0 or compact Q4_0");
     if (k <= 0 || k % 256 != 0) fail(NEMO_ERR_INVALID, "quantized matmul K must be divisible by 256");
     if (n <= 0) fail(NEMO_ERR_INVALID, "n must be positive");
     set_device(ctx);

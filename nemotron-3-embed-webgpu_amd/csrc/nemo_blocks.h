@@ -150,4 +150,46 @@ __device__ __forceinline__ void q6k_expand(const Q6KFetch& f, half8v* lo, half8v
   hi[1] = to_half8(vh + 8);
 }
 
+// Q4_0 split layout: 16 nibble bytes per 32-value block, f16 d separate.
+// Value j < 16 of a block is d (low nibble of byte j - 8), value 16 + j is
+// d (high nibble of byte j - 8) (src/gguf/quantization.ts:40-44); d (q - 8)
+// has at most 15 significant bits and is exact in fp32. For chunk k0 (a
+// multiple of 64) and part p: lo = block k0/32, hi = block k0/32 + 1, each
+// the low (p = 0) or high (p = 1) nibbles.
+struct Q40Fetch {
+  u32x4 q0, q1;
+  uint16_t d0, d1;
+  int p;
+};
+
+__device__ __forceinline__ Q40Fetch q40_fetch(const QWeight& w, size_t row_bytes, int row, int k0, int p) {
+  const int b = k0 >> 5;
+  const uint8_t* base = w.blocks + (size_t)row * row_bytes + (size_t)b * 16;
+  Q40Fetch f;
+  f.q0 = *(const u32x4*)base;
+  f.q1 = *(const u32x4*)(base + 16);
+  const uint16_t* d = w.d + (size_t)row * (w.k >> 5) + b;
+  f.d0 = d[0];
+  f.d1 = d[1];
+  f.p = p;
+  return f;
+}
+
+__device__ __forceinline__ void q40_expand(const Q40Fetch& f, half8v* lo, half8v* hi) {
+  const float d0 = h2f(f.d0), d1 = h2f(f.d1);
+  const int sh = 4 * f.p;
+  const uint32_t a[4] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w};
+  const uint32_t b[4] = {f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  float vl[16], vh[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bytes4_fma(opaque((a[i] >> sh) & 0x0f0f0f0fu), d0, -8.0f * d0, vl + 4 * i);
+    bytes4_fma(opaque((b[i] >> sh) & 0x0f0f0f0fu), d1, -8.0f * d1, vh + 4 * i);
+  }
+  lo[0] = to_half8(vl);
+  lo[1] = to_half8(vl + 8);
+  hi[0] = to_half8(vh);
+  hi[1] = to_half8(vh + 8);
+}
+
 }  // namespace nemo

@@ -46,6 +46,15 @@ struct WFetch<kQ6_K> {
   __device__ __forceinline__ void expand(half8v* lo, half8v* hi) const { q6k_expand(f, lo, hi); }
 };
 
+template <>
+struct WFetch<kQ4_0> {
+  Q40Fetch f;
+  __device__ __forceinline__ void load(const QWeight& w, size_t rb, int row, int k0, int p) {
+    f = q40_fetch(w, rb, row, k0, p);
+  }
+  __device__ __forceinline__ void expand(half8v* lo, half8v* hi) const { q40_expand(f, lo, hi); }
+};
+
 // Epilogue for a wave owning MI x 4 blocks of 32 x 32 starting at (rbase0,
 // cbase): lane l, register r of block (i, j) is row rbase0 + 32i + 8(r/4) +
 // 4(l/32) + r%4, column cbase + 32j + l%32.
@@ -487,7 +496,8 @@ static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx,
 // VALU work per weight and does best on the 4-wave LDS-staged tiles.
 static int gemm_variant(const QWeight& w, int m, int splits) {
   const int ntiles = (w.n + 127) / 128;
-  if (w.type == kQ4_K && w.n % kBigBN == 0 && ((m + kBigBM - 1) / kBigBM) * (w.n / kBigBN) * splits >= 256)
+  if ((w.type == kQ4_K || w.type == kQ4_0) && w.n % kBigBN == 0 &&
+      ((m + kBigBM - 1) / kBigBM) * (w.n / kBigBN) * splits >= 256)
     return kVarBig;
   if (w.type == kQ6_K && m >= 512) return kVarLds256;
   return (m >= 512 && ((m + 255) / 256) * ntiles * splits >= 512) ? kVarLds256 : kVarLds128;
@@ -531,7 +541,8 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (w.type == kQ4_K) expand_kernel<kQ4_K><<<blocks, 256, 0, stream>>>(w, wexp);
-  else expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
+  else if (w.type == kQ6_K) expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
+  else expand_kernel<kQ4_0><<<blocks, 256, 0, stream>>>(w, wexp);
   const int kchunk = w.k / splits;
   dim3 grid((w.n + bn - 1) / bn, (m + kBigBM - 1) / kBigBM, splits);
   if (bn == 256) launch_f16<256>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream);
@@ -545,7 +556,7 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
   if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
-  if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
+  if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
   const int bn = wexp ? two_pass_bn(w, m, splits) : 0;
   if (bn) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, bn);
@@ -556,8 +567,10 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   else launch_typed<T, kEpiSwiGLU>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);
   if (w.type == kQ4_K) {
     NEMO_LAUNCH(kQ4_K)
-  } else {
+  } else if (w.type == kQ6_K) {
     NEMO_LAUNCH(kQ6_K)
+  } else {
+    NEMO_LAUNCH(kQ4_0)
   }
 #undef NEMO_LAUNCH
   return hipGetLastError();
@@ -570,7 +583,7 @@ hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
 hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, uint16_t* y, int ldy,
                                 uint16_t* wexp, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
-  if (w.type != kQ4_K && w.type != kQ6_K) return hipErrorInvalidValue;
+  if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int bn = w.n % 256 == 0 ? 256 : 128;
   return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream, bn);
 }

@@ -17,6 +17,9 @@ enum GgmlType : int { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_K = 12, kQ6_K = 14 };
 //  Q6_K: GGUF's 210-byte blocks are split at upload so that loads stay
 //        16-byte aligned: `blocks` holds 208-byte records (ql[128] qh[64]
 //        scales[16]) and `d` the per-block f16 scale, both row major.
+//  Q4_0: likewise split (from GGUF's 18-byte blocks or the wgpack
+//        tile32-compact records): `blocks` holds the 16 nibble bytes of each
+//        32-value block, `d` its f16 scale, both row major.
 struct QWeight {
   int type;
   int n;
@@ -27,7 +30,7 @@ struct QWeight {
 
 // Bytes per row of `blocks`.
 __host__ __device__ inline size_t qweight_row_bytes(int type, int k) {
-  return type == kQ4_K ? (size_t)(k / 256) * 144 : (size_t)(k / 256) * 208;
+  return type == kQ4_K ? (size_t)(k / 256) * 144 : type == kQ6_K ? (size_t)(k / 256) * 208 : (size_t)(k / 32) * 16;
 }
 
 // GEMM epilogues.

@@ -100,12 +100,43 @@ struct GvQ6K {
   }
 };
 
+// Q4_0 (split layout): lane group kq owns values [64kq, +64) of the
+// 256-value block, i.e. the Q4_0 blocks 2kq and 2kq + 1; run r = block
+// 2kq + r/2, low (r even) or high (r odd) nibbles.
+__device__ __forceinline__ int gv_q40_run_k(int kq, int r) { return 64 * kq + 16 * r; }
+
+struct GvQ40 {
+  u32x4 q0, q1;
+  uint16_t d0, d1;
+  __device__ __forceinline__ void load(const QWeight& w, size_t row_bytes, int row, int blk, int kq) {
+    const int b = 8 * blk + 2 * kq;
+    const uint8_t* p = w.blocks + (size_t)row * row_bytes + (size_t)b * 16;
+    q0 = *(const u32x4*)p;
+    q1 = *(const u32x4*)(p + 16);
+    const uint16_t* d = w.d + (size_t)row * (w.k >> 5) + b;
+    d0 = d[0];
+    d1 = d[1];
+  }
+  __device__ __forceinline__ void run(int kq, int r, half8v& f0, half8v& f1) const {
+    const u32x4 q = (r >> 1) ? q1 : q0;
+    const float d = h2f((r >> 1) ? d1 : d0);
+    const int sh = 4 * (r & 1);
+    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bytes4_fma(opaque((words[i] >> sh) & 0x0f0f0f0fu), d, -8.0f * d, v + 4 * i);
+    f0 = to_half8(v);
+    f1 = to_half8(v + 8);
+  }
+};
+
 enum GvMode { kGvStore = 0, kGvPartial = 1, kGvSwiGLU = 2 };
 
 template <int TYPE, int MODE, int kGvTiles>
 __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w, int M,
                                                              void* __restrict__ out, int ldo) {
-  using Raw = typename std::conditional<TYPE == kQ4_K, GvQ4K, GvQ6K>::type;
+  using Raw = typename std::conditional<TYPE == kQ4_K, GvQ4K,
+                                        typename std::conditional<TYPE == kQ6_K, GvQ6K, GvQ40>::type>::type;
   // P 16-row tiles of gate-half rows and the P matching tiles 64 rows later;
   // 4 / P workgroups per 128-row group.
   constexpr int P = kGvTiles / 2, G = 4 / P;
@@ -128,7 +159,7 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
     half8v xa[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : gv_q6k_run_k(kq, r);
+      const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : TYPE == kQ6_K ? gv_q6k_run_k(kq, r) : gv_q40_run_k(kq, r);
       xa[2 * r] = *(const half8v*)(xr + k);
       xa[2 * r + 1] = *(const half8v*)(xr + k + 8);
     }
@@ -253,13 +284,14 @@ template <int MODE>
 static void launch_gemv_typed(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
                               hipStream_t stream) {
   if (w.type == kQ4_K) launch_gemv_kernel<kQ4_K, MODE>(x, ldx, w, m, out, ldo, stream);
-  else launch_gemv_kernel<kQ6_K, MODE>(x, ldx, w, m, out, ldo, stream);
+  else if (w.type == kQ6_K) launch_gemv_kernel<kQ6_K, MODE>(x, ldx, w, m, out, ldo, stream);
+  else launch_gemv_kernel<kQ4_0, MODE>(x, ldx, w, m, out, ldo, stream);
 }
 
 hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, void* out, int ldo,
                           float* partials, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
-  if (m > 16 || (w.type != kQ4_K && w.type != kQ6_K)) return hipErrorInvalidValue;
+  if (m > 16 || (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0)) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
   const int splits = gemv_splits(w);
   if (epilogue == kEpiPartial) {
@@ -437,9 +469,31 @@ __global__ void dequant_q6k_split_kernel(QWeight w, float* __restrict__ out32) {
   }
 }
 
+// Q4_0 split layout: thread per 32-value block.
+__global__ void dequant_q40_split_kernel(QWeight w, int64_t n_blocks, float* __restrict__ out32) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n_blocks) return;
+  const u32x4 q = *(const u32x4*)(w.blocks + b * 16);
+  const float d = h2f(w.d[b]);
+  const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bytes4_fma(words[i] & 0x0f0f0f0fu, d, -8.0f * d, v + 4 * i);
+    bytes4_fma((words[i] >> 4) & 0x0f0f0f0fu, d, -8.0f * d, v + 16 + 4 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) *(float4v*)(out32 + b * 32 + 4 * i) = float4v{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+}
+
 hipError_t launch_dequant_weight(const QWeight& w, float* out32, hipStream_t stream) {
   const int64_t nb = (int64_t)w.n * (w.k / 256);
   if (w.type == kQ4_K) return launch_dequant_raw(kQ4_K, w.blocks, nb, out32, nullptr, stream);
+  if (w.type == kQ4_0) {
+    const int64_t n40 = (int64_t)w.n * (w.k / 32);
+    dequant_q40_split_kernel<<<(unsigned)((n40 + 255) / 256), 256, 0, stream>>>(w, n40, out32);
+    return hipGetLastError();
+  }
   if (w.type != kQ6_K) return hipErrorInvalidValue;
   const int64_t threads = nb * 8;
   dequant_q6k_split_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(w, out32);

@@ -8,7 +8,8 @@ const { native } = require('./native');
 const { isPrepackedModel, PREPACKED_STORAGE_COMPACT } = require('./prepacked');
 
 const GGMLType = Object.freeze({ F32: 0, F16: 1, Q4_0: 2, Q4_K: 12, Q6_K: 14 });
-const NEMO_ERR_UNSUPPORTED = 5;
+// wgpack q4_0-tile32-compact records (NEMO_TYPE_Q4_0_TILE32, include/nemo.h)
+const NEMO_TYPE_Q4_0_TILE32 = 258;
 
 /** src/webgpu/model.ts:30-32 */
 function contextualMergedLength(sequence) {
@@ -42,15 +43,9 @@ function requestHipDevice(index) {
   return new HipDevice(index);
 }
 
-function unsupported(message) {
-  const error = new Error(message);
-  error.status = NEMO_ERR_UNSUPPORTED;
-  return error;
-}
-
 /**
  * new NemotronHipModel(device, source, { dims, embeddingType })
- * source: a PrepackedModel (parsePrepackedModel) with raw tensors, a
+ * source: a PrepackedModel (parsePrepackedModel; raw or q4_0-tile32-compact tensors), a
  * GGUF-like { tensors: Map(name -> { dimensions, type, byteOffset,
  * byteLength }), buffer }, or { synthetic: seed } for seeded synthetic weights.
  */
@@ -69,11 +64,9 @@ class NemotronHipModel {
       } else {
         if (!source || !(source.tensors instanceof Map)) throw new TypeError('model source must hold a tensors Map');
         for (const tensor of source.tensors.values()) {
-          if (isPrepackedModel(source) && tensor.storage === PREPACKED_STORAGE_COMPACT) {
-            throw unsupported(`${tensor.name}: compact Q4_0 tile32 matrices are not supported by this build`);
-          }
+          const compact = isPrepackedModel(source) && tensor.storage === PREPACKED_STORAGE_COMPACT;
           const bytes = new Uint8Array(source.buffer, tensor.byteOffset, tensor.byteLength);
-          addon.modelSetTensor(this.handle, tensor.name, tensor.type, tensor.dimensions, bytes);
+          addon.modelSetTensor(this.handle, tensor.name, compact ? NEMO_TYPE_Q4_0_TILE32 : tensor.type, tensor.dimensions, bytes);
         }
       }
       addon.modelFinalize(this.handle);

@@ -190,16 +190,13 @@ class NemotronHipModel:
                                                 buf.ctypes.data_as(ctypes.c_void_p), buf.size))
 
     def _load_prepacked(self, pack) -> None:
+        """src/webgpu/model.ts:263-279: every tensor of the pack is uploaded;
+        compact Q4_0 tile32 matrices as TYPE_Q4_0_TILE32 records."""
         from .prepacked import PREPACKED_STORAGE_COMPACT
-        compact = [t for t in pack.tensors.values() if t["storage"] == PREPACKED_STORAGE_COMPACT]
-        if compact:
-            # src/webgpu/model.ts:263-279 executes compact Q4_0 tile32 matrices;
-            # this build executes Q4_K / Q6_K and rejects them explicitly.
-            raise NemoError(5, f"prepacked model has {len(compact)} compact Q4_0 tile32 matrices; this runtime "
-                               "executes raw Q4_K/Q6_K tensors")
         view = memoryview(pack.buffer)
         for t in pack.tensors.values():
-            self.set_tensor(t["name"], t["type"], t["dimensions"], view[t["byteOffset"]:t["byteOffset"] + t["byteLength"]])
+            type_ = _lib.TYPE_Q4_0_TILE32 if t["storage"] == PREPACKED_STORAGE_COMPACT else t["type"]
+            self.set_tensor(t["name"], type_, t["dimensions"], view[t["byteOffset"]:t["byteOffset"] + t["byteLength"]])
 
     def get_tensor(self, name: str) -> tuple[int, list[int], bytes]:
         """(ggml_type, dims, GGUF bytes) of a tensor as held on the device."""

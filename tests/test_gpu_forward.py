@@ -147,3 +147,81 @@ def test_synthetic_model_readback_matches_oracle(torch_cuda):
     got = model.createPlan(1, 40).run_sync(np.array(seq, dtype=np.uint32), [40])[0]
     ref = oracle.forward_request(om, np.array(seq))
     assert _cos(got, ref) >= 0.9999
+
+
+def _reference_pack(dims, tensors):
+    """The reference's prepack pipeline (scripts/prepack-model.ts:28-45) on a
+    synthetic model: every projection requantized to Q4_0 (the oracle's
+    requantizeMatrixToQ40), q/k/v and gate/up fused by rows, packed as
+    tile32-compact; the token table and norms stored raw. Returns the .wgpack
+    bytes and the tensors as the oracle sees them (fused raw Q4_0)."""
+    from nemo_amd import prepacked as pp
+    raw_parts, packed, oracle_tensors = [], [], {}
+
+    def part(name):
+        t, d, data = tensors[name]
+        k, n = d
+        return {"name": name, "k": k, "n": n, "bytes": oracle.requantize_to_q40(data, t, k, n)}
+
+    for l in range(dims.layers):
+        p = f"blk.{l}."
+        for fused, names in ((p + "attn_qkv.weight", [p + "attn_qkv.weight"]),
+                             (p + "attn_output.weight", [p + "attn_output.weight"]),
+                             (p + "ffn_gate_up.weight", [p + "ffn_gate_up.weight"]),
+                             (p + "ffn_down.weight", [p + "ffn_down.weight"])):
+            parts = [part(nm) for nm in names]
+            packed.append(pp.pack_q40_tile32(fused, parts))
+            k = parts[0]["k"]
+            oracle_tensors[fused] = (2, [k, sum(q["n"] for q in parts)], b"".join(q["bytes"] for q in parts))
+    for name, (t, d, data) in tensors.items():
+        if name not in oracle_tensors:
+            raw_parts.append(pp.raw_tensor(name, d, t, data))
+            oracle_tensors[name] = (t, d, data)
+    return pp.build_prepacked_file("synthetic", 0, {"general.architecture": "mistral3"}, raw_parts + packed), \
+        oracle_tensors
+
+
+@pytest.mark.parametrize("hd", [128, 64])
+def test_compact_q40_pack_matches_oracle(torch_cuda, hd):
+    """A .wgpack in the reference's published layout (compact Q4_0 matrices,
+    Q6_K token table): parsePrepackedModel -> model -> embeddings within cosine
+    0.9999 of the oracle on the dequantized Q4_0 weights."""
+    from nemo_amd import prepacked as pp
+    Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
+    dims = rt.make_dims(hidden=256, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=768, layers=2, vocab=300,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=hd + 11, embedding_type=14)
+    pack, otensors = _reference_pack(dims, tensors)
+    model = rt.NemotronHipModel(pp.parse_prepacked_model(pack), dims=dims)
+    om = synth.oracle_model(dims, otensors)
+    seqs = [[1] + list(synth.randint(810 + i, n - 1, 2, 300)) for i, n in enumerate([40, 9, 25])]
+    ids, lens = _padded(seqs, 40)
+    got = model.createPlan(len(seqs), 40).run_sync(ids, lens)
+    for i, s in enumerate(seqs):
+        c = _cos(got[i], oracle.forward_request(om, np.array(s)))
+        assert c >= 0.9999, f"request {i}: cosine {c:.6f}"
+    # the matrices read back as the GGUF Q4_0 blocks that were packed
+    t, d, data = model.get_tensor("blk.1.ffn_down.weight")
+    assert t == 2 and data == otensors["blk.1.ffn_down.weight"][2]
+
+
+def test_reference_dims_full_batch_matches_oracle(torch_cuda):
+    """The reference model's shapes (24 query heads x 128, 8 KV heads, FFN
+    6144; src/webgpu/model.ts:19-24) at 16 requests x 150 tokens through two
+    layers: QKV 5120 rows, gate/up 12288, GQA groups of 3, head_dim 128."""
+    dims = rt.reference_dims()
+    dims.layers, dims.merge_after_layer, dims.vocab = 2, 1, 8192
+    model = rt.NemotronHipModel(None, dims=dims, synthetic_seed=4242)
+    tensors = {}
+    for name in ["token_embd.weight", "output_norm.weight"] + [f"blk.{l}.{t}.weight" for l in range(2) for t in (
+            "attn_qkv", "attn_output", "ffn_gate_up", "ffn_down", "attn_norm", "ffn_norm")]:
+        typ, d, data = model.get_tensor(name)
+        tensors[name] = (typ, [x for x in d if x != 1] or [1], data)
+    om = synth.oracle_model(dims, tensors)
+    ids = synth.randint(78, 16 * 150, 2, dims.vocab).astype(np.uint32)
+    ids[::150] = 1
+    got = model.createPlan(16, 150).run_sync(ids, [150] * 16)
+    for b in (0, 9):
+        ref = oracle.forward_request(om, ids[b * 150:(b + 1) * 150].astype(np.int64))
+        c = _cos(got[b], ref)
+        assert c >= 0.9999, f"request {b}: cosine {c:.6f}"

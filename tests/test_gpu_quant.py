@@ -180,3 +180,50 @@ def test_matmul_rejects_bad_shapes(torch_cuda):
         rt.QuantWeight(12, 1, 300, raw.tobytes())
     with pytest.raises(rt.NemoError, match="bytes; expected"):
         rt.QuantWeight(12, 3, 256, raw.tobytes())
+
+
+def _q40_pair(seed, n, k):
+    """Q4_0 raw GGUF blocks of a random n x k matrix and the same matrix in the
+    wgpack tile32-compact layout (the oracle's packQ40Tile32)."""
+    raw = synth.random_q40(seed, n * k // 32)
+    return raw, oracle.pack_q40_tile32(raw.tobytes(), k, n)
+
+
+@pytest.mark.parametrize("n,k", [(300, 512), (2048, 2048)])
+def test_q40_weights_dequantize_bit_exact(torch_cuda, n, k):
+    """Raw Q4_0 and tile32-compact uploads decode to the reference's
+    dequantizeQ40Block values (src/gguf/quantization.ts:40-44)."""
+    torch = torch_cuda
+    raw, compact = _q40_pair(6000 + n, n, k)
+    expect = oracle.dequantize(2, raw)
+    for type_, data in ((_lib.TYPE_Q4_0, raw.tobytes()), (_lib.TYPE_Q4_0_TILE32, compact)):
+        w = rt.QuantWeight(type_, n, k, data)
+        out = torch.empty(n * k, dtype=torch.float32, device="cuda")
+        w.dequantize(out.data_ptr())
+        torch.cuda.synchronize()
+        assert _bits_equal(out.cpu().numpy(), expect), f"type {type_}"
+
+
+@pytest.mark.parametrize("m,n,k", [(15, 2048, 2048), (16, 12288, 2048), (150, 5120, 2048), (2400, 2048, 6144),
+                                   (333, 200, 768)])
+def test_q40_matmul_all_paths(torch_cuda, m, n, k):
+    """The compact Q4_0 matrices of the reference's pack through the GEMV (m <=
+    16), the fused GEMM and the two-pass GEMM: within the projection bar of
+    the oracle, and GEMM and two-pass bit-identical."""
+    torch = torch_cuda
+    raw, compact = _q40_pair(7000 + m + n, n, k)
+    w = rt.QuantWeight(_lib.TYPE_Q4_0_TILE32, n, k, compact)
+    x16 = synth.normal(7001 + m, m * k).astype(np.float16).reshape(m, k)
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    algos = [_lib.MATMUL_GEMM, _lib.MATMUL_TWO_PASS] + ([_lib.MATMUL_GEMV] if m <= 16 else [])
+    outs = {}
+    for algo in algos:
+        dy = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+        w.matmul(dx.data_ptr(), m, dy.data_ptr(), algo)
+        torch.cuda.synchronize()
+        outs[algo] = dy.cpu().numpy()
+    assert np.array_equal(outs[_lib.MATMUL_GEMM], outs[_lib.MATMUL_TWO_PASS])
+    cols = np.sort(synth.randint(7002 + n, min(n, 256), 0, n))
+    w32 = oracle.dequantize(2, raw).reshape(n, k)[cols]
+    for algo, y in outs.items():
+        _check_matmul(y.view(np.float16)[:, cols], x16, w32)
