@@ -229,6 +229,10 @@ struct nemo_ctx {
 
 struct LayerWeights {
   QWeight qkv, o, gate_up, down;
+  // q, k and v of different GGML types (a Q4_K_M file stores attn_v as Q6_K)
+  // stay separate: each part writes its column range of the QKV buffer.
+  // Empty when `qkv` holds the fused matrix.
+  std::vector<std::pair<QWeight, int>> qkv_parts;
   const float* attn_norm = nullptr;
   const float* ffn_norm = nullptr;
 };
@@ -505,9 +509,21 @@ nemo_status nemo_model_finalize(nemo_model* model) {
     std::vector<LayerWeights> layers(d.layers);
     for (int l = 0; l < d.layers; ++l) {
       const std::string p = "blk." + std::to_string(l) + ".";
-      fuse_rows(model, p + "attn_qkv.weight", {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"});
+      const std::string qn = p + "attn_q.weight", kn = p + "attn_k.weight", vn = p + "attn_v.weight";
+      const bool mixed_qkv = !model->tensors.count(p + "attn_qkv.weight") && model->tensors.count(qn) &&
+                             model->tensors.count(kn) && model->tensors.count(vn) &&
+                             (model->tensors[qn].type != model->tensors[kn].type ||
+                              model->tensors[qn].type != model->tensors[vn].type);
+      if (mixed_qkv) {
+        const int64_t KW = (int64_t)d.kv_heads * d.head_dim;
+        layers[l].qkv_parts = {{matrix(model, qn, H, QW), 0},
+                               {matrix(model, kn, H, KW), (int)QW},
+                               {matrix(model, vn, H, KW), (int)(QW + KW)}};
+      } else {
+        fuse_rows(model, p + "attn_qkv.weight", {qn, kn, vn});
+        layers[l].qkv = matrix(model, p + "attn_qkv.weight", H, QKV);
+      }
       fuse_rows(model, p + "ffn_gate_up.weight", {p + "ffn_gate.weight", p + "ffn_up.weight"});
-      layers[l].qkv = matrix(model, p + "attn_qkv.weight", H, QKV);
       layers[l].o = matrix(model, p + "attn_output.weight", QW, H);
       matrix(model, p + "ffn_gate_up.weight", H, 2 * F);  // validates before reordering
       DevTensor& gu = model->tensors[p + "ffn_gate_up.weight"];
@@ -650,24 +666,39 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->ffn = dev_alloc(tf * F * 2, "SwiGLU output");
     // fp32 split-K partial sums of the projections that split K.
     size_t partial_floats = 0;
+    auto qkv_matrices = [](const LayerWeights& w) {
+      std::vector<const QWeight*> v;
+      if (w.qkv_parts.empty()) v.push_back(&w.qkv);
+      for (const auto& part : w.qkv_parts) v.push_back(&part.first);
+      return v;
+    };
     for (const LayerWeights& w : model->layers) {
-      for (const QWeight* q : {&w.qkv, &w.o, &w.down}) {
+      std::vector<const QWeight*> mats = qkv_matrices(w);
+      mats.push_back(&w.o);
+      mats.push_back(&w.down);
+      for (const QWeight* q : mats) {
         const int s = gemm_splits(*q);
         if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
       }
     }
     // Passes of at most 16 tokens take the GEMV, whose split counts differ.
     const size_t small_m = std::min<size_t>(tf, 16);
-    for (const LayerWeights& w : model->layers)
-      for (const QWeight* q : {&w.qkv, &w.o, &w.gate_up, &w.down})
+    for (const LayerWeights& w : model->layers) {
+      std::vector<const QWeight*> mats = qkv_matrices(w);
+      mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
+      for (const QWeight* q : mats)
         partial_floats = std::max(partial_floats, (size_t)gemv_splits(*q) * small_m * q->n);
+    }
     if (partial_floats) p->partials = dev_alloc(partial_floats * 4, "split-K partial sums");
     // f16 expansion of the largest matrix that takes the two-pass GEMM.
     size_t wexp_halves = 0;
-    for (const LayerWeights& w : model->layers)
-      for (const QWeight* q : {&w.qkv, &w.o, &w.gate_up, &w.down})
+    for (const LayerWeights& w : model->layers) {
+      std::vector<const QWeight*> mats = qkv_matrices(w);
+      mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
+      for (const QWeight* q : mats)
         if (gemm_two_pass(*q, (int)tf, gemm_splits(*q)))
           wexp_halves = std::max(wexp_halves, (size_t)q->n * q->k);
+    }
     if (wexp_halves) p->wexp = dev_alloc(wexp_halves * 2, "f16 weight expansion");
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
     const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
@@ -794,15 +825,20 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // At most 16 tokens: the split-K GEMV (HBM-bound; the MFMA tiles would
     // leave most CUs idle). Its results are independent of M too.
     const bool small = M <= 16;
-    const int qkv_splits = gemm_splits(w.qkv);
-    if (small) {
-      hip_check(launch_gemv_ex(norm, H, w.qkv, M, kEpiStore, qkv, QKV, partials, s), "qkv gemv");
-    } else if (qkv_splits == 1) {
-      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiStore, 1, qkv, QKV, s, wexp), "qkv matmul");
-    } else {
-      hip_check(launch_gemm_ex(norm, H, w.qkv, M, kEpiPartial, qkv_splits, partials, QKV, s, wexp), "qkv matmul");
-      hip_check(launch_reduce_partials(partials, qkv_splits, M, QKV, qkv, QKV, s), "qkv reduce");
-    }
+    // One matrix, or separate q / k / v parts each into its column range.
+    auto qkv_proj = [&](const QWeight& wq, int col) {
+      const int sp = gemm_splits(wq);
+      if (small) {
+        hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
+      } else if (sp == 1) {
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp), "qkv matmul");
+      } else {
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s, wexp), "qkv matmul");
+        hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
+      }
+    };
+    if (w.qkv_parts.empty()) qkv_proj(w.qkv, 0);
+    for (const auto& part : w.qkv_parts) qkv_proj(part.first, part.second);
     mark(2, false);
     mark(3, true);
     hip_check(launch_rope(qkv, QKV, rows, rope, d.q_heads, d.kv_heads, d.head_dim, q, k, s), "rope");

@@ -46,7 +46,7 @@ export declare class NemotronHipPlan implements EmbeddingPlan {
 }
 
 export declare class NemotronHipModel implements EmbeddingRuntime {
-  constructor(device: HipDevice, source: TensorSource | PrepackedModel | { synthetic: number },
+  constructor(device: HipDevice, source: TensorSource | PrepackedModel | GGUFModel | { synthetic: number },
               options?: { dims?: Partial<ModelDims>; embeddingType?: number });
   readonly dims: ModelDims;
   readonly maxStorageBufferBindingSize?: number;
@@ -81,3 +81,22 @@ export declare function rawTensor(name: string, dimensions: number[], type: numb
 export declare function buildPrepackedFile(sourceSha256: string, sourceBytes: number, metadata: Record<string, unknown>,
                                            tensors: PackedTensorBytes[]): Uint8Array;
 export declare function parsePrepackedModel(buffer: ArrayBuffer): PrepackedModel;
+
+// GGUF (src/gguf/reader.ts, src/gguf/types.ts)
+export type GGUFScalar = string | number | bigint | boolean;
+export type GGUFMetadataValue = GGUFScalar | GGUFScalar[];
+export interface GGUFTensorInfo {
+  name: string; dimensions: number[]; type: number; offset: number; byteOffset: number; byteLength: number;
+  elementCount: number;
+}
+export interface GGUFModel {
+  version: number; alignment: number; metadata: Map<string, GGUFMetadataValue>; tensors: Map<string, GGUFTensorInfo>;
+  dataOffset: number; buffer: ArrayBuffer;
+}
+export declare class GGUFReader {
+  constructor(buffer: ArrayBuffer);
+  parse(options?: { metadataKeys?: ReadonlySet<string> }): GGUFModel;
+}
+export declare function tensorByteLength(type: number, elements: number): number;
+export declare function dimsFromMetadata(model: GGUFModel, base: ModelDims): ModelDims;
+export declare const NEMOTRON3_METADATA_KEYS: ReadonlySet<string>;

@@ -5,6 +5,7 @@
 const runtime = require('./runtime');
 const prepacked = require('./prepacked');
 const engine = require('./engine');
+const gguf = require('./gguf');
 const { native, ADDON_PATH } = require('./native');
 
-module.exports = Object.assign({ native, ADDON_PATH }, runtime, prepacked, engine);
+module.exports = Object.assign({ native, ADDON_PATH }, runtime, prepacked, engine, gguf);

@@ -53,7 +53,9 @@ class NemotronHipModel {
   constructor(device, source, options) {
     const opts = options || {};
     this.device = device;
-    this.dims = Object.assign(referenceDims(), opts.dims || {});
+    const isGguf = source && source.metadata instanceof Map && typeof source.dataOffset === 'number' && !source.header;
+    const base = isGguf && !opts.dims ? require('./gguf').dimsFromMetadata(source, referenceDims()) : referenceDims();
+    this.dims = Object.assign(base, opts.dims || {});
     // No per-binding storage cap on HIP: the engine's storage split never triggers.
     this.maxStorageBufferBindingSize = undefined;
     const addon = native();

@@ -151,9 +151,10 @@ class NemotronHipPlan:
 class NemotronHipModel:
     """Weights on one device; implements EmbeddingRuntime.
 
-    ``source`` is a ``PrepackedModel`` (src/prepacked/format.ts:54-59) whose
-    tensors are stored raw, a mapping name -> (ggml_type, dims, bytes), or
-    None together with ``synthetic_seed`` for seeded synthetic weights.
+    ``source`` is a ``PrepackedModel`` (src/prepacked/format.ts:54-59), a
+    parsed ``GGUFModel`` (src/gguf/types.ts:37-44; dims default to its
+    metadata), a mapping name -> (ggml_type, dims, bytes), or None together
+    with ``synthetic_seed`` for seeded synthetic weights.
     """
 
     # No per-binding storage limit on HIP: the engine's storage cap does not
@@ -163,6 +164,10 @@ class NemotronHipModel:
     def __init__(self, source=None, dims: Dims | None = None, device: int = 0, synthetic_seed: int | None = None,
                  embedding_type: int = TYPE_F16):
         self.ctx = HipContext.shared(device)
+        is_gguf = hasattr(source, "dataOffset") and hasattr(source, "metadata") and hasattr(source, "version")
+        if dims is None and is_gguf:
+            from .gguf import dims_from_metadata
+            dims = dims_from_metadata(source)
         self.dims = dims if dims is not None else reference_dims()
         self.hidden = self.dims.hidden
         self._ptr = ctypes.c_void_p()
@@ -174,6 +179,13 @@ class NemotronHipModel:
             check(L.nemo_model_synthesize(self._ptr, int(synthetic_seed), int(embedding_type)))
         elif hasattr(source, "header") and hasattr(source, "tensors"):
             self._load_prepacked(source)
+        elif is_gguf:
+            # src/webgpu/model.ts:281-304: every tensor uploaded, q/k/v and
+            # gate/up fused at finalize
+            view = memoryview(source.buffer)
+            for t in source.tensors.values():
+                self.set_tensor(t["name"], t["type"], t["dimensions"],
+                                view[t["byteOffset"]:t["byteOffset"] + t["byteLength"]])
         else:
             for name, (ggml_type, dims_, data) in source.items():
                 self.set_tensor(name, ggml_type, dims_, data)

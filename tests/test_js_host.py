@@ -35,3 +35,37 @@ def test_js_host_and_cross_language_pack(tmp_path):
     norm = pp.raw_tensor("norm", [4], 0, bytes([7] * 16))
     want = pp.build_prepacked_file("feed", 123, {"general.name": "cross"}, [norm, packed])
     assert out.read_bytes() == want
+
+
+def test_js_gguf_reader_matches_python(tmp_path):
+    """The JS host's GGUFReader and the Python one agree on a file with every
+    metadata value type and every tensor type; 64-bit values are BigInt in JS
+    (src/gguf/reader.ts:121-130)."""
+    import json
+    import sys
+    sys.path.insert(0, HERE)
+    from gguf_writer import nemotron_metadata, write_gguf
+    from test_gguf import _sample
+    from nemo_amd import gguf, runtime as rt
+    md, tensors = _sample(64)
+    d = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, layers=2, vocab=40)
+    md += nemotron_metadata(d)
+    tensors.append(("token_embd.weight", [256, 40], 1, bytes(256 * 40 * 2)))
+    path = tmp_path / "m.gguf"
+    path.write_bytes(write_gguf(md, tensors, alignment=64))
+    py = gguf.GGUFReader(path.read_bytes()).parse()
+    js = json.loads(_node("gguf_dump.js", str(path)))
+    assert (js["version"], js["alignment"], js["dataOffset"]) == (py.version, py.alignment, py.dataOffset)
+    assert js["tensors"] == list(py.tensors.values())
+    for key, value in py.metadata.items():
+        got = js["metadata"][key]
+        if key in ("a.u64", "a.i64"):
+            assert got == f"bigint:{value}"
+        elif isinstance(value, float):
+            assert got == pytest.approx(value)
+        else:
+            assert got == value
+    assert js["dims"]["hidden"] == 256 and js["dims"]["layers"] == 2 and js["dims"]["vocab"] == 40
+    assert js["dims"]["mergeAfterLayer"] == 2
+    filtered = json.loads(_node("gguf_dump.js", str(path), "filter"))
+    assert set(filtered["metadata"]) <= gguf.NEMOTRON3_METADATA_KEYS
