@@ -187,6 +187,18 @@ nemo_status nemo_weight_dequantize(nemo_weight* weight, float* d_out, void* stre
 nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_values, float* d_out_f32,
                             uint16_t* d_out_f16, void* stream);
 
+/* ---- offline requantization (src/gguf/quantization.ts:77-131) ------------ */
+
+/* requantizeMatrixToQ40 (src/gguf/quantization.ts:101-131) on the GPU: the
+ * raw GGUF bytes of an n x k matrix of type Q4_K, Q6_K or Q4_0 (host memory,
+ * n_src bytes) -> n * k / 32 GGUF Q4_0 blocks of 18 bytes written to `out`
+ * (host memory, out_bytes). Bit-exact with the reference's JavaScript, which
+ * quantizes each 32 values as quantizeQ40Block (:77-98). Errors as the
+ * reference: "K=<k> is not divisible by a K-quant block", "source has <n>
+ * bytes; expected <m>". scripts/prepack-model.ts:28-36 calls it per matrix. */
+nemo_status nemo_requantize_q40(nemo_ctx* ctx, int32_t src_type, const void* src, size_t n_src, int64_t k, int64_t n,
+                                void* out, size_t out_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1050,3 +1050,26 @@ nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_valu
   });
 }
 
+
+nemo_status nemo_requantize_q40(nemo_ctx* ctx, int32_t src_type, const void* src, size_t n_src, int64_t k, int64_t n,
+                                void* out, size_t out_bytes) {
+  return guarded([&] {
+    if (!ctx || !src || !out) fail(NEMO_ERR_INVALID, "null argument");
+    if (src_type != kQ4_K && src_type != kQ6_K && src_type != kQ4_0)
+      fail(NEMO_ERR_UNSUPPORTED, "requantization reads Q4_K, Q6_K or Q4_0");
+    if (k <= 0 || n <= 0) fail(NEMO_ERR_INVALID, "k and n must be positive");
+    if (k % 256) fail(NEMO_ERR_INVALID, "K=" + std::to_string(k) + " is not divisible by a K-quant block");
+    const size_t expect = src_type == kQ4_0 ? (size_t)n * (k / 32) * 18 : (size_t)n * (k / 256) * (src_type == kQ4_K ? 144 : 210);
+    if (n_src != expect)
+      fail(NEMO_ERR_INVALID, "source has " + std::to_string(n_src) + " bytes; expected " + std::to_string(expect));
+    const size_t need = (size_t)n * (k / 32) * 18;
+    if (out_bytes < need) fail(NEMO_ERR_INVALID, "output needs " + std::to_string(need) + " bytes");
+    set_device(ctx);
+    DevPtr d_src = dev_alloc(n_src, "requantize source");
+    DevPtr d_out = dev_alloc(need, "requantize output");
+    hip_check(hipMemcpy(d_src.get(), src, n_src, hipMemcpyHostToDevice), "upload");
+    hip_check(launch_requant_q40(src_type, (const uint8_t*)d_src.get(), k, n, (uint8_t*)d_out.get(), nullptr),
+              "requantize");
+    hip_check(hipMemcpy(out, d_out.get(), need, hipMemcpyDeviceToHost), "download");
+  });
+}

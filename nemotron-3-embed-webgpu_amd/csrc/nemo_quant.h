@@ -89,6 +89,12 @@ hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
 hipError_t launch_dequant_raw(int type, const uint8_t* raw, int64_t n_blocks, float* out_f32,
                               uint16_t* out_f16, hipStream_t stream);
 
+// requantizeMatrixToQ40 on the device: raw GGUF Q4_K / Q6_K / Q4_0 rows of a
+// k x n matrix (k % 256 == 0) -> n * k / 32 GGUF Q4_0 blocks (18 bytes),
+// bit-exact with the reference's JavaScript (nemo_requant.hip).
+hipError_t launch_requant_q40(int src_type, const uint8_t* src, int64_t k, int64_t n, uint8_t* out,
+                              hipStream_t stream);
+
 // Decode an uploaded weight (any layout above) to float32 [n, k].
 hipError_t launch_dequant_weight(const QWeight& w, float* out_f32, hipStream_t stream);
 

@@ -100,3 +100,7 @@ export declare class GGUFReader {
 export declare function tensorByteLength(type: number, elements: number): number;
 export declare function dimsFromMetadata(model: GGUFModel, base: ModelDims): ModelDims;
 export declare const NEMOTRON3_METADATA_KEYS: ReadonlySet<string>;
+
+/** scripts/prepack-model.ts: GGUF bytes -> .wgpack bytes (Q4_0 tile32 projections, requantized on the GPU). */
+export declare function prepackGGUF(source: Uint8Array, requantize?: (type: number, bytes: Uint8Array, k: number, n: number) => Uint8Array,
+                                    device?: number): Uint8Array;

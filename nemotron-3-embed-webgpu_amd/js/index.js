@@ -6,6 +6,7 @@ const runtime = require('./runtime');
 const prepacked = require('./prepacked');
 const engine = require('./engine');
 const gguf = require('./gguf');
+const prepack = require('./prepack');
 const { native, ADDON_PATH } = require('./native');
 
-module.exports = Object.assign({ native, ADDON_PATH }, runtime, prepacked, engine, gguf);
+module.exports = Object.assign({ native, ADDON_PATH }, runtime, prepacked, engine, gguf, prepack);

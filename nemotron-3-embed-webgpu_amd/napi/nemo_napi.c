@@ -474,6 +474,32 @@ static napi_value js_plan_profile(napi_env env, napi_callback_info info) {
   return o;
 }
 
+/* requantizeQ40(ctx, srcType, bytes, k, n) -> Uint8Array of n * k / 32
+ * GGUF Q4_0 blocks (requantizeMatrixToQ40, src/gguf/quantization.ts:101-131,
+ * on the GPU). Blocking. */
+static napi_value js_requantize_q40(napi_env env, napi_callback_info info) {
+  napi_value argv[5], ab, out;
+  int32_t type;
+  double kd, nd;
+  void* src;
+  size_t n_src;
+  if (!get_args(env, info, 5, argv)) return NULL;
+  handle_t* h = unwrap(env, argv[0], 1);
+  if (!h || !get_i32(env, argv[1], &type) || !get_bytes(env, argv[2], &src, &n_src)) return NULL;
+  if (napi_get_value_double(env, argv[3], &kd) != napi_ok || napi_get_value_double(env, argv[4], &nd) != napi_ok) {
+    napi_throw_type_error(env, NULL, "k and n must be numbers");
+    return NULL;
+  }
+  const int64_t k = (int64_t)kd, n = (int64_t)nd;
+  const size_t need = k > 0 && n > 0 ? (size_t)n * (size_t)(k / 32) * 18 : 0;
+  void* dst = NULL;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, need ? need : 1, &dst, &ab));
+  nemo_status s = nemo_requantize_q40((nemo_ctx*)h->ptr, type, src, n_src, k, n, dst, need);
+  if (s) return throw_status(env, s);
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_uint8_array, need, ab, 0, &out));
+  return out;
+}
+
 static napi_value module_init(napi_env env, napi_value exports) {
   const napi_property_descriptor props[] = {
       {"version", NULL, js_version, NULL, NULL, NULL, napi_enumerable, NULL},
@@ -490,6 +516,7 @@ static napi_value module_init(napi_env env, napi_value exports) {
       {"planRun", NULL, js_plan_run, NULL, NULL, NULL, napi_enumerable, NULL},
       {"planProfile", NULL, js_plan_profile, NULL, NULL, NULL, napi_enumerable, NULL},
       {"planDestroy", NULL, js_plan_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"requantizeQ40", NULL, js_requantize_q40, NULL, NULL, NULL, napi_enumerable, NULL},
   };
   if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;
   return exports;

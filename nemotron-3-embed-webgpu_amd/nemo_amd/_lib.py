@@ -26,6 +26,7 @@ EXPORTED = [
     "nemo_plan_profile", "nemo_profile_stage_count", "nemo_profile_stage_name", "nemo_plan_destroy",
     "nemo_plan_read_buffer",
     "nemo_weight_create", "nemo_weight_destroy", "nemo_weight_matmul", "nemo_weight_dequantize", "nemo_dequantize",
+    "nemo_requantize_q40",
 ]
 
 
@@ -88,6 +89,7 @@ def load() -> ctypes.CDLL:
         "nemo_weight_matmul": (i32, [vp, vp, i32, vp, i32, vp]),
         "nemo_weight_dequantize": (i32, [vp, vp, vp]),
         "nemo_dequantize": (i32, [i32, vp, ctypes.c_int64, vp, vp, vp]),
+        "nemo_requantize_q40": (i32, [vp, i32, vp, sz, ctypes.c_int64, ctypes.c_int64, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

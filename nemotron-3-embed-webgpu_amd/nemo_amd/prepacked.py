@@ -12,6 +12,7 @@ import json
 import math
 import struct
 from dataclasses import dataclass
+from decimal import Decimal
 
 MAGIC = b"WGPACK02"
 PRELUDE_BYTES = 12
@@ -44,6 +45,50 @@ class PrepackedModel:
     tensors: dict   # name -> header entry plus "byteOffset"
     buffer: bytes
     dataOffset: int  # noqa: N815 (reference field name)
+
+
+def _js_number_text(x: float) -> str:
+    """Number::toString (ECMA-262 6.1.6.1.20) of a double: the shortest
+    round-trip digits, fixed notation for 1e-7 <= |x| < 1e21, else
+    exponential with an explicit exponent sign."""
+    if x != x or x in (float("inf"), float("-inf")):
+        return "null"  # JSON.stringify writes non-finite numbers as null
+    if x == 0:
+        return "0"
+    sign = "-" if x < 0 else ""
+    digits_tuple = Decimal(repr(abs(x))).normalize().as_tuple()
+    digits = "".join(str(d) for d in digits_tuple.digits)
+    k = len(digits)
+    n = digits_tuple.exponent + k
+    if k <= n <= 21:
+        text = digits + "0" * (n - k)
+    elif 0 < n <= 21:
+        text = digits[:n] + "." + digits[n:]
+    elif -6 < n <= 0:
+        text = "0." + "0" * (-n) + digits
+    else:
+        e = n - 1
+        mant = digits if k == 1 else digits[0] + "." + digits[1:]
+        text = f"{mant}e{'+' if e >= 0 else '-'}{abs(e)}"
+    return sign + text
+
+
+def js_json(value) -> str:
+    """JSON.stringify(value): compact, UTF-8 text (control characters
+    escaped), numbers as JavaScript writes them."""
+    if isinstance(value, bool) or value is None:
+        return json.dumps(value)
+    if isinstance(value, int):
+        return str(value)
+    if isinstance(value, float):
+        return _js_number_text(value)
+    if isinstance(value, str):
+        return json.dumps(value, ensure_ascii=False)
+    if isinstance(value, dict):
+        return "{" + ",".join(json.dumps(str(k), ensure_ascii=False) + ":" + js_json(v) for k, v in value.items()) + "}"
+    if isinstance(value, (list, tuple)):
+        return "[" + ",".join(js_json(v) for v in value) + "]"
+    raise TypeError(f"cannot serialize {type(value).__name__}")
 
 
 def pack_q40_tile32(name: str, parts: list[dict]) -> PackedTensorBytes:
@@ -99,7 +144,7 @@ def build_prepacked_file(source_sha256: str, source_bytes: int, metadata: dict,
     header = {"version": 2, "sourceSha256": source_sha256, "sourceBytes": source_bytes, "layout": PREPACKED_LAYOUT,
               "tileRows": PREPACKED_TILE_ROWS, "blockValues": PREPACKED_BLOCK_VALUES,
               "blockBytes": PREPACKED_BLOCK_BYTES, "metadata": metadata, "tensors": entries}
-    header_bytes = json.dumps(header, separators=(",", ":")).encode()
+    header_bytes = js_json(header).encode()
     data_offset = _align(PRELUDE_BYTES + len(header_bytes), DATA_ALIGNMENT)
     out = bytearray(data_offset + relative)
     out[0:8] = MAGIC

@@ -273,8 +273,19 @@ def dequantize_device(ggml_type: int, d_raw: int, n_values: int, d_out_f32: int 
                                       ctypes.c_void_p(d_out_f16 or None), ctypes.c_void_p(stream or None)))
 
 
+def requantize_q40(src_type: int, data, k: int, n: int, device: int = 0) -> bytes:
+    """requantizeMatrixToQ40 (src/gguf/quantization.ts:101-131) on the GPU:
+    raw GGUF Q4_K / Q6_K / Q4_0 bytes of an n x k matrix -> GGUF Q4_0 bytes."""
+    ctx = HipContext.shared(device)
+    src = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+    out = np.empty(n * (k // 32) * 18, dtype=np.uint8)
+    check(_lib.load().nemo_requantize_q40(ctx.ptr, int(src_type), src.ctypes.data_as(ctypes.c_void_p), src.size,
+                                          int(k), int(n), out.ctypes.data_as(ctypes.c_void_p), out.size))
+    return out.tobytes()
+
+
 __all__ = [
     "TYPE_F16", "TYPE_F32", "TYPE_Q4_0", "TYPE_Q4_K", "TYPE_Q6_K", "Dims", "NemoError", "HipContext",
     "NemotronHipModel", "NemotronHipPlan", "QuantWeight", "contextual_merged_length", "reference_dims",
-    "config_dims", "make_dims", "dequantize_device",
+    "config_dims", "make_dims", "dequantize_device", "requantize_q40",
 ]

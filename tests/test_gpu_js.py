@@ -33,3 +33,20 @@ def test_js_host_on_gpu(tmp_path):
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "4/4 passed" in r.stdout
+
+
+def test_js_prepack_matches_python(tmp_path):
+    """node js/prepack.js on a GGUF gives the same .wgpack bytes as the
+    Python tool (both requantize on the GPU)."""
+    from gguf_writer import nemotron_metadata, write_gguf
+    from nemo_amd import prepack
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=256, layers=2, vocab=64,
+                        merge_after_layer=2)
+    t = synth.model_tensors(dims, seed=17, embedding_type=14, fused=False)
+    src = tmp_path / "m.gguf"
+    src.write_bytes(write_gguf(nemotron_metadata(dims), [(n, d, ty, b) for n, (ty, d, b) in t.items()]))
+    out = tmp_path / "m.wgpack"
+    script = os.path.join(os.path.dirname(HERE), "nemotron-3-embed-webgpu_amd", "js", "prepack.js")
+    r = subprocess.run([NODE, script, str(src), str(out)], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert out.read_bytes() == prepack.prepack_gguf(src.read_bytes())

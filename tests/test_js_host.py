@@ -69,3 +69,18 @@ def test_js_gguf_reader_matches_python(tmp_path):
     assert js["dims"]["mergeAfterLayer"] == 2
     filtered = json.loads(_node("gguf_dump.js", str(path), "filter"))
     assert set(filtered["metadata"]) <= gguf.NEMOTRON3_METADATA_KEYS
+
+
+def test_pack_header_json_matches_javascript():
+    """The Python pack builder writes its JSON header as JSON.stringify does
+    (number formatting, UTF-8 text), so both hosts produce identical packs."""
+    import json
+    import random
+    from nemo_amd.prepacked import js_json
+    rng = random.Random(5)
+    vals = [1e6, 9.999999747378752e-06, 1e21, 1e20, 1e-7, 1.2e-7, 5e-324, 1.7976931348623157e308, -0.5, 65504.0]
+    vals += [rng.uniform(-1, 1) * 10 ** rng.randint(-30, 30) for _ in range(500)]
+    value = {"v": vals, "s": "héllo\n\t\u0001\"x\\", "i": [0, -3, 2 ** 52], "b": [True, False, None]}
+    r = subprocess.run([NODE, "-e", "process.stdout.write(JSON.stringify(" + json.dumps(value) + "))"],
+                       capture_output=True, text=True, timeout=60)
+    assert js_json(value) == r.stdout
