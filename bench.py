@@ -2,6 +2,7 @@
 Nemotron-3-Embed encoder on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W]
+python bench.py --matrix [--tokens T] [--matrix-weights q4_0|q4_k]
 
 One step = one execution-plan run over one batch of 16 requests x 150 tokens
 (token ids and embeddings resident in HBM; the host hands over only the
@@ -19,6 +20,17 @@ Printed JSON (one line on stdout):
   cpu_baseline the oracle's CPU forward of the same encoder (float64 numpy,
                binary16 storage) on a bounded sample of the workload
 Progress goes to stderr.
+
+--matrix runs the reference's published comparison instead (README.md:15-24,
+src/main.ts:244-313) at the reference model's shape (hidden 2048, 24 query
+heads x 128, 8 KV heads, FFN 6144, 16 layers): for 15/50/150/500/1500/5000
+tokens, requests/s of one request at a time and of 16 at once in native
+batches, through plan.run with host buffers (upload and readback included,
+as in the reference), next to the published Apple M3 Max WebGPU figures;
+then the same rows through the micro-batching engine under the reference's
+closed-loop harness (scripts/bench-lib.ts) at concurrency 1 and 16. Weights
+are seeded synthetic Q4_0 blocks (the published pack's storage) or the
+device-synthesized Q4_K/Q6_K set; one JSON line with every row.
 """
 from __future__ import annotations
 
@@ -40,6 +52,11 @@ HBM_PEAK_GBS = 8000.0
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# README.md:17-22: WebGPU req/s on Apple M3 Max (30-core GPU), single / 16x
+PUBLISHED_M3_MAX = {15: (69.68, 266.02), 50: (48.80, 93.89), 150: (24.03, 32.55), 500: (8.18, 9.50),
+                    1500: (2.56, 2.75), 5000: (0.76, 0.72)}
 
 
 def workload_ids(vocab: int):
@@ -214,6 +231,104 @@ def kernel_rates(torch, stream) -> dict:
     return out
 
 
+def synthetic_q40_tensors(dims, seed: int) -> dict:
+    """Seeded synthetic weights in the published pack's storage: every
+    projection Q4_0 (random nibbles; scales of either sign near 0.0053, what
+    N(0, 0.02) blocks quantize to), an f16 N(0, 0.02) token table, norms 1."""
+    import numpy as np
+    from nemo_amd._lib import TYPE_F16, TYPE_F32, TYPE_Q4_0
+    rng = np.random.default_rng(seed)
+    H, F = dims.hidden, dims.intermediate
+    QKV = (dims.q_heads + 2 * dims.kv_heads) * dims.head_dim
+    QW = dims.q_heads * dims.head_dim
+
+    def q40(k, n):
+        blocks = n * (k // 32)
+        raw = rng.integers(0, 256, size=(blocks, 18), dtype=np.uint8)
+        d = (rng.choice(np.array([-1.0, 1.0]), blocks) * 0.0053 * (1 + 0.1 * rng.standard_normal(blocks)))
+        raw[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(blocks, 2)
+        return TYPE_Q4_0, [k, n], raw.reshape(-1)
+
+    ones = np.ones(H, dtype=np.float32)
+    table = np.empty((dims.vocab, H), dtype=np.float16)
+    for r in range(0, dims.vocab, 8192):
+        rows = min(8192, dims.vocab - r)
+        table[r:r + rows] = rng.standard_normal((rows, H), dtype=np.float32) * np.float32(0.02)
+    t = {"token_embd.weight": (TYPE_F16, [H, dims.vocab], table.reshape(-1)),
+         "output_norm.weight": (TYPE_F32, [H], ones)}
+    for layer in range(dims.layers):
+        p = f"blk.{layer}."
+        t[p + "attn_norm.weight"] = (TYPE_F32, [H], ones)
+        t[p + "ffn_norm.weight"] = (TYPE_F32, [H], ones)
+        t[p + "attn_qkv.weight"] = q40(H, QKV)
+        t[p + "attn_output.weight"] = q40(QW, H)
+        t[p + "ffn_gate_up.weight"] = q40(H, 2 * F)
+        t[p + "ffn_down.weight"] = q40(F, H)
+    return t
+
+
+def run_matrix(args) -> int:
+    """The comparison matrix and the closed-loop engine rows (module doc)."""
+    import asyncio
+    import torch
+    from nemo_amd import benchlib
+    from nemo_amd import runtime as rt
+    from nemo_amd.engine import NemotronEmbeddingEngine
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dims = rt.reference_dims()
+    counts = benchlib.COMPARISON_TOKEN_COUNTS if not args.tokens else (args.tokens,)
+    if any(c not in PUBLISHED_M3_MAX for c in counts):
+        raise SystemExit(f"unsupported matrix token count {args.tokens}")
+    t0 = time.perf_counter()
+    if args.matrix_weights == "q4_0":
+        log("building seeded Q4_0 weights at the reference model's shape")
+        model = rt.NemotronHipModel(synthetic_q40_tensors(dims, SEED), dims=dims)
+    else:
+        log("synthesizing Q4_K/Q6_K weights at the reference model's shape on the device")
+        model = rt.NemotronHipModel(None, dims=dims, synthetic_seed=SEED, embedding_type=rt.TYPE_F16)
+    log(f"model ready in {time.perf_counter() - t0:.1f} s")
+    tokenizer = benchlib.WordTokenizer(dims.vocab)
+    loop = asyncio.new_event_loop()
+    rows = loop.run_until_complete(benchlib.comparison_matrix(model, tokenizer, counts, write=log))
+    for r in rows:
+        single, concurrent = PUBLISHED_M3_MAX[r["exactTokens"]]
+        r["publishedM3Max"] = {"singleRps": single, "aggregateRps": concurrent}
+        r["vsPublished"] = {"single": round(r["singleRps"] / single, 2),
+                            "aggregate": round(r["aggregateRps"] / concurrent, 2)}
+
+    engine_rows = []
+    if args.engine_duration_ms > 0:
+        class EngineTarget:
+            name = "nemotron-hip-engine"
+
+            def __init__(self):
+                self.engine = NemotronEmbeddingEngine(model, tokenizer)
+
+            async def embed(self, text):
+                return await self.engine.embed(text)
+
+        for exact in counts:
+            workload = benchlib.comparison_workload(exact)
+            for concurrency in (1, 16):
+                res = loop.run_until_complete(benchlib.benchmark_target(EngineTarget(), benchlib.BenchmarkOptions(
+                    concurrency, args.engine_duration_ms, 3, workload["inputs"], exact)))
+                log(f"engine {exact} tokens x{concurrency}: {res['requestsPerSecond']:.2f} req/s, "
+                    f"p50 {res['latencyMs']['p50']:.2f} ms, errors {res['errors']}")
+                engine_rows.append(dict(res, exactTokens=exact))
+    print(json.dumps({
+        "metric": "comparison matrix: requests/s single and 16 concurrent (plan.run, host buffers)",
+        "unit": "requests/s", "n_gpus": 1, "dtype": "f16", "higher_is_better": True,
+        "data": f"synthetic ({args.matrix_weights} weights, seed {SEED}; 'vector' x (T-1) after BOS)",
+        "config": {"workload": "comparison matrix, reference model shape", "hidden": dims.hidden,
+                   "q_heads": dims.q_heads, "kv_heads": dims.kv_heads, "head_dim": dims.head_dim,
+                   "intermediate": dims.intermediate, "layers": dims.layers, "vocab": dims.vocab,
+                   "weights": args.matrix_weights},
+        "published_reference": "README.md:17-22, WebGPU on Apple M3 Max (30-core GPU)",
+        "rows": rows, "engine_closed_loop": engine_rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,11 +336,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the GEMV / dequant measurements")
+    ap.add_argument("--matrix", action="store_true", help="run the published comparison matrix instead")
+    ap.add_argument("--tokens", type=int, default=0, help="--matrix: one row (15, 50, 150, 500, 1500 or 5000)")
+    ap.add_argument("--matrix-weights", choices=("q4_0", "q4_k"), default="q4_0")
+    ap.add_argument("--engine-duration-ms", type=float, default=2000.0,
+                    help="--matrix: closed-loop engine run per row and concurrency (0 skips)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the encoder pass on a single MI355X "
-              "(requests are independent; see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "(requests are independent: more GPUs would each take whole micro-batches).", file=sys.stderr)
         return 2
+    if args.matrix:
+        return run_matrix(args)
 
     import numpy as np
     import torch
