@@ -1010,7 +1010,7 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
     if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
     set_device(weight->ctx);
     hipStream_t s = (hipStream_t)stream;
-    if (algo < 0 || algo > 3) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+    if (algo < 0 || algo > 4) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
     const QWeight& w = weight->w;
     const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= 16);
     const bool two_pass =
@@ -1018,6 +1018,8 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
     if (gemv) {
       if (m > 16) fail(NEMO_ERR_INVALID, "GEMV takes m <= 16");
       hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)weight->partials.get(), s), "gemv");
+    } else if (algo == NEMO_MATMUL_GEMM_MID) {
+      hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
     } else if (two_pass) {
       if (!weight->wexp) weight->wexp = dev_alloc((size_t)w.n * w.k * 2, "f16 weight expansion");
       hip_check(launch_gemm_two_pass(d_x, w.k, w, m, d_y, w.n, (uint16_t*)weight->wexp.get(), s), "two-pass gemm");

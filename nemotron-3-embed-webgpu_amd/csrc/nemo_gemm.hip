@@ -179,6 +179,137 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Mid-size batches: 64 x 128 x 64 tiles, 4 waves (2 along M x 2 along N) of
+// 32 rows x 64 columns. Wave (wm, wn) owns column blocks wn and wn + 2 of
+// 32, so the gate and up rows of the same features (64 apart in the
+// interleaved gate/up layout) meet in one wave for the SwiGLU epilogue. With
+// few workgroups per CU a step is bound by memory latency, which the
+// 1-step-ahead loads of gemm_kernel expose every step; here the raw X and W
+// bytes of the next kMidDepth - 1 steps are in flight in registers while a
+// step decodes into LDS (double-buffered, one barrier per step) and runs its
+// MFMAs. The MFMA sequence per output element is the one above.
+// ---------------------------------------------------------------------------
+
+constexpr int kMidDepth = 4, kMidBM = 64;
+
+template <int TYPE, int EPI>
+// (x is not __restrict__: a restrict read-only pointer's loads may move across
+// the compiler fences below.)
+__global__ __launch_bounds__(256) void gemm_mid_kernel(const uint16_t* x, int ldx, QWeight w, int M,
+                                                       int kchunk, void* __restrict__ out, int ldo) {
+  constexpr int BM = kMidBM, BN = 128, D = kMidDepth;
+  static_assert(D % 2 == 0, "the LDS buffer of step s + u is u % 2");
+  __shared__ __attribute__((aligned(16))) half_t sA[2][BM * kLdsK];
+  __shared__ __attribute__((aligned(16))) half_t sB[2][BN * kLdsK];
+  const int N = w.n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int kbeg = blockIdx.z * kchunk;
+  const int nsteps = kchunk / kBK;
+  const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
+
+  // X: 4 threads per row, 32 bytes each; W: 2 threads per weight row.
+  const int xr = tid >> 2, xc = (tid & 3) * 16;
+  const uint16_t* xrow = x + (size_t)min(m0 + xr, M - 1) * ldx + xc;
+  const int wr = tid >> 1, wp = tid & 1;
+  const int wrow = min(n0 + wr, N - 1);
+
+  u32x4 xa[D][2];
+  WFetch<TYPE> wf[D];
+  auto kat = [&](int s) { return kbeg + min(s, nsteps - 1) * kBK; };
+  auto fetch = [&](int slot, int k0) {
+    xa[slot][0] = *(const u32x4*)(xrow + k0);
+    xa[slot][1] = *(const u32x4*)(xrow + k0 + 8);
+    wf[slot].load(w, row_bytes, wrow, k0, wp);
+  };
+
+  float16v acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+
+  // Loads are issued in step order, which the waits count on: neither the
+  // optimizer (memory clobber) nor the scheduler may move them across steps.
+  auto fence = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int i = 0; i < D - 1; ++i) {
+    fetch(i, kat(i));
+    fence();
+  }
+  for (int s = 0; s < nsteps; s += D) {  // nsteps is a multiple of D (host check)
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      // Each step's decode stays in its step: hoisted into an earlier one it
+      // would wait there for loads that are meant to still be in flight.
+      fence();
+      half8v lo[2], hi[2];
+      wf[u].expand(lo, hi);
+      half_t* arow = &sA[u & 1][xr * kLdsK + xc];
+      *(u32x4*)arow = xa[u][0];
+      *(u32x4*)(arow + 8) = xa[u][1];
+      half_t* brow = &sB[u & 1][wr * kLdsK];
+      *(half8v*)(brow + 16 * wp) = lo[0];
+      *(half8v*)(brow + 16 * wp + 8) = lo[1];
+      *(half8v*)(brow + 32 + 16 * wp) = hi[0];
+      *(half8v*)(brow + 32 + 16 * wp + 8) = hi[1];
+      fence();
+      fetch((u + D - 1) % D, kat(s + u + D - 1));
+      fence();
+      __syncthreads();
+      const half_t* as = sA[u & 1];
+      const half_t* bs = sB[u & 1];
+#pragma unroll
+      for (int ks = 0; ks < kBK / 16; ++ks) {
+        const int kk = ks * 16 + (lane >> 5) * 8;
+        const half8v af = *(const half8v*)&as[(wm * 32 + (lane & 31)) * kLdsK + kk];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const half8v bf = *(const half8v*)&bs[((wn + 2 * j) * 32 + (lane & 31)) * kLdsK + kk];
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[j], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // lane l, register r: row 32 wm + 8 (r / 4) + 4 (l / 32) + r % 4, column
+  // 32 (wn + 2 j) + l % 32 of the tile (gemm_epilogue's layout).
+  const int rbase = m0 + wm * 32 + 4 * (lane >> 5);
+  if constexpr (EPI == kEpiSwiGLU) {
+    const int col = (n0 >> 1) + 32 * wn + (lane & 31);
+    uint16_t* y = (uint16_t*)out;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = rbase + 8 * (r >> 2) + (r & 3);
+      if (row < M) {
+        const float g = (float)(half_t)acc[0][r];
+        const float u = (float)(half_t)acc[1][r];
+        y[(size_t)row * ldo + col] = f2h(g / (1.0f + expf(-g)) * u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + 32 * (wn + 2 * j) + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = rbase + 8 * (r >> 2) + (r & 3);
+        if (row >= M) continue;
+        if constexpr (EPI == kEpiStore)
+          ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[j][r]);
+        else
+          ((float*)out)[((size_t)blockIdx.z * M + row) * ldo + col] = acc[j][r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Large tiles: 256 x 256 x 64, 8 waves (4 along M x 2 along N), each 64 x 128,
 // two waves per SIMD so one wave's decode overlaps the other's MFMAs.
 //  * X: each K step's 256 x 64 tile is copied HBM/L2 -> LDS by
@@ -468,7 +599,7 @@ int gemm_splits(const QWeight& w) {
   return s;
 }
 
-enum GemmVariant { kVarBig = 0, kVarLds128 = 1, kVarLds256 = 2 };
+enum GemmVariant { kVarBig = 0, kVarLds128 = 1, kVarLds256 = 2, kVarMid = 3 };
 
 template <int TYPE, int EPI>
 static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx, const QWeight& w, int kchunk,
@@ -482,6 +613,9 @@ static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx,
     }
     dim3 grid((w.n + kBigBN - 1) / kBigBN, (m + kBigBM - 1) / kBigBM, splits);
     gemm_big_kernel<TYPE, EPI><<<grid, 512, kBigLds, s>>>(x, ldx, w, m, kchunk, out, ldo);
+  } else if (var == kVarMid && (kchunk / kBK) % kMidDepth == 0) {
+    dim3 grid((w.n + 127) / 128, (m + kMidBM - 1) / kMidBM, splits);
+    gemm_mid_kernel<TYPE, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
   } else if (var == kVarLds256) {
     dim3 grid((w.n + 127) / 128, (m + 255) / 256, splits);
     gemm_kernel<TYPE, 256, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
@@ -501,6 +635,14 @@ static int gemm_variant(const QWeight& w, int m, int splits) {
     return kVarBig;
   if (w.type == kQ6_K && m >= 512) return kVarLds256;
   return (m >= 512 && ((m + 255) / 256) * ntiles * splits >= 512) ? kVarLds256 : kVarLds128;
+}
+
+// The 64-row deep-prefetch tiles while they give at most two workgroups per
+// CU: there a step's latency, not the machine's throughput, bounds the other
+// kernels (measured on the encoder's shapes, 17 <= m <= 1024).
+static bool use_mid(const QWeight& w, int m, int splits) {
+  const int steps = w.k / splits / kBK;
+  return steps % kMidDepth == 0 && ((m + kMidBM - 1) / kMidBM) * ((w.n + 127) / 128) * splits <= 512;
 }
 
 // Tile width of the two-pass GEMM for this problem, or 0 when the fused
@@ -550,17 +692,18 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream, uint16_t* wexp) {
+static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
+                               void* out, int ldo, hipStream_t stream, uint16_t* wexp, int forced) {
   if (m <= 0) return hipSuccess;
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
   if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
   if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
-  const int bn = wexp ? two_pass_bn(w, m, splits) : 0;
+  if (forced < 0 && use_mid(w, m, splits)) forced = kVarMid;
+  const int bn = (wexp && forced < 0) ? two_pass_bn(w, m, splits) : 0;
   if (bn) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, bn);
-  const int var = gemm_variant(w, m, splits);
+  const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
 #define NEMO_LAUNCH(T)                                                                                              \
   if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
   else if (epilogue == kEpiPartial) launch_typed<T, kEpiPartial>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream); \
@@ -574,6 +717,16 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   }
 #undef NEMO_LAUNCH
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
+                          int ldo, hipStream_t stream, uint16_t* wexp) {
+  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, wexp, -1);
+}
+
+hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
+                           int ldo, hipStream_t stream) {
+  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, nullptr, kVarMid);
 }
 
 hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, hipStream_t stream) {

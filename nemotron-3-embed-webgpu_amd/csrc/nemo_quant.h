@@ -63,6 +63,10 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 // results are bit-identical to the fused kernels'.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
                           int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
+// launch_gemm_ex on the 64-row deep-prefetch tiles whatever the size
+// (bit-identical to the other fused kernels).
+hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
+                           int ldo, hipStream_t stream);
 
 // y[m, n] = f16(sum over s of partials[s][m][n]) in split order.
 hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,

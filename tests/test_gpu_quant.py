@@ -174,6 +174,42 @@ def test_two_pass_bit_identical_to_fused(torch_cuda, type_, m, n, k):
     _check_matmul(y[:, cols], x16, w_sample)
 
 
+@pytest.mark.parametrize("type_,m,n,k", [
+    (12, 17, 5120, 2048),      # QKV of one 17-token request
+    (12, 150, 12288, 2048),    # gate/up of one 150-token request
+    (14, 96, 2048, 6144),      # down after the merge
+    (2, 50, 2048, 3072),       # Q4_0 attention output
+    (12, 333, 200, 768),       # ragged rows and columns: clamped tile edges
+    (14, 65, 384, 512),
+    (2, 1, 128, 256),          # one row, one K block
+])
+def test_mid_tiles_bit_identical_to_fused(torch_cuda, type_, m, n, k):
+    """The 64-row deep-prefetch tiles issue the same f16 operands in the same
+    MFMA order as the other fused kernels and the two-pass GEMM:
+    bit-identical results at every size, within the projection bar of the
+    oracle."""
+    torch = torch_cuda
+    seed = 8101 + m + n + type_
+    gen = {12: synth.random_q4k, 14: synth.random_q6k, 2: synth.random_q40}[type_]
+    raw = gen(seed, n * k // (32 if type_ == 2 else 256))
+    x16 = synth.normal(seed + 7, m * k).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(type_, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    outs = {}
+    for algo in (_lib.MATMUL_GEMM, _lib.MATMUL_GEMM_MID, _lib.MATMUL_TWO_PASS):
+        dy = torch.full((m, n), 0x7E00, dtype=torch.int16, device="cuda")  # NaN fill: every element written
+        w.matmul(dx.data_ptr(), m, dy.data_ptr(), algo)
+        torch.cuda.synchronize()
+        outs[algo] = dy.cpu().numpy()
+    assert np.array_equal(outs[_lib.MATMUL_GEMM], outs[_lib.MATMUL_GEMM_MID])
+    assert np.array_equal(outs[_lib.MATMUL_TWO_PASS], outs[_lib.MATMUL_GEMM_MID])
+    y = outs[_lib.MATMUL_GEMM_MID].view(np.float16)
+    assert np.all(np.isfinite(y))
+    cols = np.sort(synth.randint(seed + 9, min(n, 256), 0, n))
+    w32 = oracle.dequantize(type_, raw).reshape(n, k)[cols]
+    _check_matmul(y[:, cols], x16, w32)
+
+
 def test_matmul_rejects_bad_shapes(torch_cuda):
     raw = synth.random_q4k(1, 2)
     with pytest.raises(rt.NemoError, match="divisible by 256"):
