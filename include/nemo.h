@@ -171,6 +171,9 @@ nemo_status nemo_weight_destroy(nemo_weight* weight);
                                   then an f16 MFMA GEMM; bit-identical to NEMO_MATMUL_GEMM */
 #define NEMO_MATMUL_GEMM_MID 4 /* the fused GEMM on 64-row tiles with deep prefetch (the plan's choice
                                   for mid-size m); bit-identical to NEMO_MATMUL_GEMM */
+#define NEMO_MATMUL_GEMM_SPLIT 5 /* the 64-row tiles with K split into fp32 partials summed in chunk
+                                    order (the plan's choice for 17..64 rows); scratch is held by the
+                                    weight and grows on demand */
 
 /* Y[m, n] = f16(X[m, k] W[n, k]^T), fp32 accumulate; d_x f16 [m, k] and d_y
  * f16 [m, n] are device pointers (createRun + dispatch,

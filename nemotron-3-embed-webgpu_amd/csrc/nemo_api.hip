@@ -255,6 +255,8 @@ struct nemo_weight {
   QWeight w{};
   DevPtr partials;
   DevPtr wexp;  // f16 expansion for the two-pass GEMM, allocated on first use
+  DevPtr split_partials;  // split-K sums of NEMO_MATMUL_GEMM_SPLIT, grown on demand
+  size_t split_floats = 0;
 };
 
 struct nemo_plan {
@@ -681,6 +683,18 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
         if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
       }
     }
+    // Passes of 17 to kSplitMaxM tokens split K further on the 64-row tiles.
+    if (tf > 16) {
+      const size_t split_m = std::min<size_t>(tf, kSplitMaxM);
+      for (const LayerWeights& w : model->layers) {
+        std::vector<const QWeight*> mats = qkv_matrices(w);
+        mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
+        for (const QWeight* q : mats) {
+          const int sp = mid_splits(*q);
+          if (sp > 1) partial_floats = std::max(partial_floats, (size_t)sp * split_m * q->n);
+        }
+      }
+    }
     // Passes of at most 16 tokens take the GEMV, whose split counts differ.
     const size_t small_m = std::min<size_t>(tf, 16);
     for (const LayerWeights& w : model->layers) {
@@ -823,13 +837,24 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     const LayerWeights& w = m->layers[l];
     mark(2, true);
     // At most 16 tokens: the split-K GEMV (HBM-bound; the MFMA tiles would
-    // leave most CUs idle). Its results are independent of M too.
+    // leave most CUs idle). Up to kSplitMaxM tokens (one 64-row tile): K
+    // split into mid_splits chunks, reduced in chunk order. Each regime's
+    // split counts depend on the weight's shape only, so within a regime a
+    // token's result does not depend on the rest of the batch.
     const bool small = M <= 16;
+    const bool split_mid = !small && M <= kSplitMaxM;
     // One matrix, or separate q / k / v parts each into its column range.
     auto qkv_proj = [&](const QWeight& wq, int col) {
-      const int sp = gemm_splits(wq);
+      const int sp = split_mid ? mid_splits(wq) : gemm_splits(wq);
       if (small) {
         hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
+      } else if (split_mid) {
+        if (sp == 1) {
+          hip_check(launch_gemm_mid(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s), "qkv matmul");
+        } else {
+          hip_check(launch_gemm_mid(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s), "qkv matmul");
+          hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
+        }
       } else if (sp == 1) {
         hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp), "qkv matmul");
       } else {
@@ -849,12 +874,16 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
     auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
-      const int splits = small ? gemv_splits(wt) : gemm_splits(wt);
+      const int splits = small ? gemv_splits(wt) : split_mid ? mid_splits(wt) : gemm_splits(wt);
       mark(stage, true);
       if (small)
         hip_check(launch_gemv_ex(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial,
                                  splits == 1 ? (void*)delta : (void*)partials, H, nullptr, s),
                   "residual gemv");
+      else if (split_mid)
+        hip_check(launch_gemm_mid(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial, splits,
+                                  splits == 1 ? (void*)delta : (void*)partials, H, s),
+                  "residual matmul");
       else if (splits == 1)
         hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wexp), "residual matmul");
       else
@@ -869,10 +898,19 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     };
     residual(attn, QW, w.o, w.ffn_norm, 4);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
-    if (small)
+    if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
-    else
+    } else if (split_mid) {
+      const int sp = mid_splits(w.gate_up);
+      if (sp == 1) {
+        hip_check(launch_gemm_mid(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s), "gate/up matmul");
+      } else {
+        hip_check(launch_gemm_mid(norm, H, w.gate_up, M, kEpiPartial, sp, partials, w.gate_up.n, s), "gate/up matmul");
+        hip_check(launch_reduce_swiglu(partials, sp, M, w.gate_up.n, ffn, F, s), "gate/up reduce");
+      }
+    } else {
       hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
+    }
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
     residual(ffn, F, w.down, next, 8);
@@ -1010,7 +1048,7 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
     if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
     set_device(weight->ctx);
     hipStream_t s = (hipStream_t)stream;
-    if (algo < 0 || algo > 4) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+    if (algo < 0 || algo > 5) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
     const QWeight& w = weight->w;
     const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= 16);
     const bool two_pass =
@@ -1020,6 +1058,22 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
       hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)weight->partials.get(), s), "gemv");
     } else if (algo == NEMO_MATMUL_GEMM_MID) {
       hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
+    } else if (algo == NEMO_MATMUL_GEMM_SPLIT) {
+      const int sp = mid_splits(w);
+      if (sp == 1) {
+        hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
+      } else {
+        const size_t need = (size_t)sp * m * w.n;
+        if (need > weight->split_floats) {
+          if (s) hip_check(hipStreamSynchronize(s), "sync");
+          weight->split_partials.reset();
+          weight->split_partials = dev_alloc(need * 4, "split-K partial sums");
+          weight->split_floats = need;
+        }
+        float* part = (float*)weight->split_partials.get();
+        hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiPartial, sp, part, w.n, s), "gemm");
+        hip_check(launch_reduce_partials(part, sp, m, w.n, d_y, w.n, s), "reduce");
+      }
     } else if (two_pass) {
       if (!weight->wexp) weight->wexp = dev_alloc((size_t)w.n * w.k * 2, "f16 weight expansion");
       hip_check(launch_gemm_two_pass(d_x, w.k, w, m, d_y, w.n, (uint16_t*)weight->wexp.get(), s), "two-pass gemm");

@@ -19,6 +19,8 @@
 // K order is the same in every kernel (sequential 16-column MFMA steps on the
 // same f16 operands), so all paths give identical bits and a
 // token's result does not depend on how many other tokens share the batch.
+#include <algorithm>
+
 #include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_quant.h"
@@ -596,6 +598,17 @@ int gemm_splits(const QWeight& w) {
   if (ntiles >= 24) return 1;
   int s = 1;
   while (s < 4 && kblocks % (2 * s) == 0 && w.k / (2 * s) >= 1024) s *= 2;
+  return s;
+}
+
+int mid_splits(const QWeight& w) {
+  // K chunks of at least 512 columns, enough of them that a single 64-row
+  // tile of the matrix gives 512 workgroups, and a divisor of the block count.
+  const int kblocks = w.k / 256, ntiles = (w.n + 127) / 128;
+  const int cap = std::max(1, std::min(w.k / 512, (512 + ntiles - 1) / ntiles));
+  int s = 1;
+  for (int c = 1; c <= cap; ++c)
+    if (kblocks % c == 0) s = c;
   return s;
 }
 

@@ -63,6 +63,11 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 // results are bit-identical to the fused kernels'.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
                           int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
+// K-split count of the small-batch regime (17 <= m <= kSplitMaxM rows, one
+// 64-row tile): a function of the weight's shape only.
+int mid_splits(const QWeight& w);
+constexpr int kSplitMaxM = 64;
+
 // launch_gemm_ex on the 64-row deep-prefetch tiles whatever the size
 // (bit-identical to the other fused kernels).
 hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
@@ -71,6 +76,10 @@ hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, 
 // y[m, n] = f16(sum over s of partials[s][m][n]) in split order.
 hipError_t launch_reduce_partials(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
                                   hipStream_t stream);
+// SwiGLU of the gate/up projection from its split-K partials
+// ([splits][m][n], rows interleaved per 128-row group): y[m, n / 2] f16.
+hipError_t launch_reduce_swiglu(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
+                                hipStream_t stream);
 
 // Small-M path (m <= 16): MFMA GEMV, 64 rows x 2048 K per workgroup with an
 // in-workgroup reduction; K beyond 2048 splits into fp32 partials summed in

@@ -254,6 +254,15 @@ __global__ void reduce_swiglu_kernel(const float* __restrict__ partials, int spl
   y[(size_t)m * ldy + f] = f2h(g / (1.0f + expf(-g)) * u);
 }
 
+hipError_t launch_reduce_swiglu(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
+                                hipStream_t stream) {
+  const int64_t total = (int64_t)m * (n / 2);
+  if (total <= 0) return hipSuccess;
+  if (n % 128) return hipErrorInvalidValue;
+  reduce_swiglu_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(partials, splits, m, n, y, ldy);
+  return hipGetLastError();
+}
+
 int gemv_splits(const QWeight& w) {
   // One workgroup row covers 8 blocks (2048 values) of K.
   return ((w.k >> 8) + kGvWaves - 1) / kGvWaves;
@@ -308,10 +317,7 @@ hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   if (partials == nullptr) return hipErrorInvalidValue;
   launch_gemv_typed<kGvPartial>(x, ldx, w, m, partials, w.n, stream);
   if (epilogue == kEpiStore) return launch_reduce_partials(partials, splits, m, w.n, (uint16_t*)out, ldo, stream);
-  const int64_t total = (int64_t)m * (w.n / 2);
-  reduce_swiglu_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(partials, splits, m, w.n, (uint16_t*)out,
-                                                                            ldo);
-  return hipGetLastError();
+  return launch_reduce_swiglu(partials, splits, m, w.n, (uint16_t*)out, ldo, stream);
 }
 
 hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m, float* partials,

@@ -16,7 +16,7 @@ STATUS_NAMES = {1: "invalid", 2: "missing", 3: "device", 4: "out of memory", 5: 
 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 12, 14
 TYPE_Q4_0_TILE32 = 258  # wgpack q4_0-tile32-compact records (include/nemo.h)
-MATMUL_AUTO, MATMUL_GEMM, MATMUL_GEMV, MATMUL_TWO_PASS, MATMUL_GEMM_MID = 0, 1, 2, 3, 4
+MATMUL_AUTO, MATMUL_GEMM, MATMUL_GEMV, MATMUL_TWO_PASS, MATMUL_GEMM_MID, MATMUL_GEMM_SPLIT = 0, 1, 2, 3, 4, 5
 
 # Every symbol include/nemo.h declares.
 EXPORTED = [

@@ -210,6 +210,38 @@ def test_mid_tiles_bit_identical_to_fused(torch_cuda, type_, m, n, k):
     _check_matmul(y[:, cols], x16, w32)
 
 
+@pytest.mark.parametrize("type_,m,n,k", [
+    (12, 17, 5120, 2048),      # QKV: 4 chunks of 512
+    (14, 200, 2048, 6144),     # down: 12 chunks
+    (2, 64, 2048, 3072),       # Q4_0 attention output: 6 chunks
+    (12, 256, 12288, 2048),    # gate/up at the regime's largest batch
+    (14, 33, 384, 512),        # one chunk: the unsplit tiles
+])
+def test_split_k_tiles_match_oracle(torch_cuda, type_, m, n, k):
+    """The small-batch regime's split-K tiles (fp32 chunk sums reduced in
+    chunk order): within the projection bar of the oracle, and the same
+    bits on every call."""
+    torch = torch_cuda
+    seed = 8201 + m + n + type_
+    gen = {12: synth.random_q4k, 14: synth.random_q6k, 2: synth.random_q40}[type_]
+    raw = gen(seed, n * k // (32 if type_ == 2 else 256))
+    x16 = synth.normal(seed + 7, m * k).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(type_, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    outs = []
+    for _ in range(2):
+        dy = torch.full((m, n), 0x7E00, dtype=torch.int16, device="cuda")
+        w.matmul(dx.data_ptr(), m, dy.data_ptr(), _lib.MATMUL_GEMM_SPLIT)
+        torch.cuda.synchronize()
+        outs.append(dy.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    y = outs[0].view(np.float16)
+    assert np.all(np.isfinite(y))
+    cols = np.sort(synth.randint(seed + 9, min(n, 256), 0, n))
+    w32 = oracle.dequantize(type_, raw).reshape(n, k)[cols]
+    _check_matmul(y[:, cols], x16, w32)
+
+
 def test_matmul_rejects_bad_shapes(torch_cuda):
     raw = synth.random_q4k(1, 2)
     with pytest.raises(rt.NemoError, match="divisible by 256"):
