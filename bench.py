@@ -2,7 +2,7 @@
 Nemotron-3-Embed encoder on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W]
-python bench.py --matrix [--tokens T] [--matrix-weights q4_0|q4_k]
+python bench.py --matrix [--tokens T] [--matrix-weights q4_0|q4_k] [--tokenizer tokenizer.json]
 
 One step = one execution-plan run over one batch of 16 requests x 150 tokens
 (token ids and embeddings resident in HBM; the host hands over only the
@@ -288,7 +288,11 @@ def run_matrix(args) -> int:
         log("synthesizing Q4_K/Q6_K weights at the reference model's shape on the device")
         model = rt.NemotronHipModel(None, dims=dims, synthetic_seed=SEED, embedding_type=rt.TYPE_F16)
     log(f"model ready in {time.perf_counter() - t0:.1f} s")
-    tokenizer = benchlib.WordTokenizer(dims.vocab)
+    if args.tokenizer:
+        from nemo_amd.tokenizer import load_tokenizer
+        tokenizer = load_tokenizer(args.tokenizer)  # the model's tokenizer.json: exact lengths are checked
+    else:
+        tokenizer = benchlib.WordTokenizer(dims.vocab)
     loop = asyncio.new_event_loop()
     rows = loop.run_until_complete(benchlib.comparison_matrix(model, tokenizer, counts, write=log))
     for r in rows:
@@ -339,6 +343,7 @@ def main() -> int:
     ap.add_argument("--matrix", action="store_true", help="run the published comparison matrix instead")
     ap.add_argument("--tokens", type=int, default=0, help="--matrix: one row (15, 50, 150, 500, 1500 or 5000)")
     ap.add_argument("--matrix-weights", choices=("q4_0", "q4_k"), default="q4_0")
+    ap.add_argument("--tokenizer", default="", help="--matrix: a local tokenizer.json (default: one token per word)")
     ap.add_argument("--engine-duration-ms", type=float, default=2000.0,
                     help="--matrix: closed-loop engine run per row and concurrency (0 skips)")
     args = ap.parse_args()
