@@ -487,25 +487,36 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
   *(half8v*)(dst + 40) = hi[1];
 }
 
-// LDS of the f16 GEMM: two stages of the 256 x 64 X tile and the BN x 64 W
-// tile (128 bytes per row): 128 KB for BN 256, 96 KB for BN 128.
-constexpr int f16_lds_bytes(int bn) { return 2 * kBigXStage + 2 * bn * 128; }
+// s_waitcnt immediate waiting for at most `n` outstanding vector memory
+// operations (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 
-template <int EPI, int BN>
-__global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
-                                                                    const uint16_t* __restrict__ wt, int N, int K,
-                                                                    int M, int kchunk, void* __restrict__ out,
-                                                                    int ldo) {
-  // 4 waves along M (64 rows each) x BN/128 along N (128 columns each).
-  constexpr int WAVES = 4 * BN / 128, MI = 2;
-  constexpr int XI = 256 / 8 / WAVES, WI = BN / 8 / WAVES;  // copy instructions per wave and stage
-  constexpr int WSTAGE = BN * 128;
+// gemm_f16_kernel<EPI, BN, WM, MI>: BM x BN x 64 tiles, BM = 32 MI WM, with
+// WM waves along M (32 MI rows each) x BN/128 along N (128 columns each).
+// LDS: two stages of the BM x 64 X tile and the BN x 64 W tile (128 bytes
+// per row). Configurations: 256 x 256 (8 waves of 64 x 128), 256 x 128 (4
+// waves of 64 x 128), 192 x 256 and 128 x 256 (4 waves of 96 or 64 x 128):
+// the tile grid is chosen per problem so the last round of workgroups is as
+// full as possible, and every configuration issues the same MFMA sequence
+// per output element.
+constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
+
+template <int EPI, int BN, int WM, int MI>
+__global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                                     const uint16_t* __restrict__ wt, int N, int K,
+                                                                     int M, int kchunk, void* __restrict__ out,
+                                                                     int ldo) {
+  constexpr int WAVES = WM * BN / 128, BM = 32 * MI * WM;
+  constexpr int XI = BM / 8 / WAVES, WI = BN / 8 / WAVES;  // copy instructions per wave and stage
+  static_assert(XI * 8 * WAVES == BM && WI * 8 * WAVES == BN, "copies must cover the tiles");
+  constexpr int XSTAGE = BM * 128, WSTAGE = BN * 128;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* sX = smem;                   // [2][256 rows][128 B]
-  uint8_t* sW = smem + 2 * kBigXStage;  // [2][BN rows][128 B]
+  uint8_t* sX = smem;               // [2][BM rows][128 B]
+  uint8_t* sW = smem + 2 * XSTAGE;  // [2][BN rows][128 B]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
-  const int m0 = blockIdx.y * kBigBM, n0 = blockIdx.x * BN;
+  const int wm = wave % WM, wn = wave / WM;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int kbeg = blockIdx.z * kchunk;
   const int nsteps = kchunk / kBK;
 
@@ -528,7 +539,7 @@ __global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint1
 #pragma unroll
     for (int i = 0; i < XI; ++i)
       __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + k0),
-                                       (lds_void*)(sX + stage * kBigXStage + (8 * XI * wave + 8 * i) * 128), 16, 0, 0);
+                                       (lds_void*)(sX + stage * XSTAGE + (8 * XI * wave + 8 * i) * 128), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < WI; ++i)
       __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + k0),
@@ -544,7 +555,7 @@ __global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint1
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   auto mfma_step = [&](int stage) {
-    const uint8_t* xs = sX + stage * kBigXStage;
+    const uint8_t* xs = sX + stage * XSTAGE;
     const uint8_t* ws = sW + stage * WSTAGE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -552,7 +563,7 @@ __global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint1
       half8v af[MI], bf[4];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int r = wm * 64 + i * 32 + (lane & 31);
+        const int r = wm * 32 * MI + i * 32 + (lane & 31);
         af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
       }
 #pragma unroll
@@ -573,8 +584,7 @@ __global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint1
   auto kat = [&](int s) { return kbeg + min(s, nsteps - 1) * kBK; };
   copy(0, kat(0));
   copy(1, kat(1));
-  if constexpr (XI + WI == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(XI + WI));
   __syncthreads();
   for (int s = 0; s < nsteps; s += 2) {
     mfma_step(0);
@@ -587,7 +597,7 @@ __global__ __launch_bounds__(4 * BN / 128 * 64) void gemm_f16_kernel(const uint1
     copy(1, kat(s + 3));
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gemm_epilogue<EPI, MI>(acc, m0 + wm * 64, n0 + wn * 128, lane, M, N, out, ldo);
+  gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo);
 }
 
 int gemm_splits(const QWeight& w) {
@@ -658,40 +668,55 @@ static bool use_mid(const QWeight& w, int m, int splits) {
   return steps % kMidDepth == 0 && ((m + kMidBM - 1) / kMidBM) * ((w.n + 127) / 128) * splits <= 512;
 }
 
-// Tile width of the two-pass GEMM for this problem, or 0 when the fused
-// kernels are the better choice (measured on the encoder's shapes): 256-column
-// tiles once they alone give every CU a workgroup; 128-column tiles for
+// f16 GEMM tile configurations of the two-pass path.
+enum F16Tile { kF16None = 0, kF16T256x256, kF16T256x128, kF16T192x256, kF16T128x256 };
+static int f16_bm(int t) { return t == kF16T192x256 ? 192 : t == kF16T128x256 ? 128 : 256; }
+static int f16_bn(int t) { return t == kF16T256x128 ? 128 : 256; }
+
+// Tile of the two-pass GEMM for this problem, or kF16None when the fused
+// kernels are the better choice (measured on the encoder's shapes): 256 x 256
+// tiles once they alone give every CU a workgroup; 256 x 128 tiles for
 // unsplit problems with at least 64 of them (the QKV projection). Split-K
 // problems with fewer 256-column tiles do better on the fused 128-row tiles,
 // of which two or more fit on a CU.
-static int two_pass_bn(const QWeight& w, int m, int splits) {
+static int two_pass_tile(const QWeight& w, int m, int splits) {
   const int mt = (m + kBigBM - 1) / kBigBM;
-  if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= 256) return 256;
-  if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) return 128;
-  return 0;
+  if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= 256) {
+    // 192-row tiles (4 waves; measured at ~0.83 of the 256-row tiles' rate
+    // per flop) when their rounds of 256 workgroups cost less: 1536 tokens
+    // give 384 tiles of 256 rows (two rounds, the second half empty) but 512
+    // of 192 rows (two full rounds of tiles 3/4 the size). Time per round is
+    // taken as tile area / rate: 0.75 / 0.83 = 0.904 of a 256-row round.
+    const int t256 = mt * (w.n / 256), t192 = ((m + 191) / 192) * (w.n / 256);
+    if (splits == 1 && 904 * ((t192 + 255) / 256) < 1000 * ((t256 + 255) / 256)) return kF16T192x256;
+    return kF16T256x256;
+  }
+  if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) return kF16T256x128;
+  return kF16None;
 }
 
-bool gemm_two_pass(const QWeight& w, int m, int splits) { return two_pass_bn(w, m, splits) != 0; }
+bool gemm_two_pass(const QWeight& w, int m, int splits) { return two_pass_tile(w, m, splits) != kF16None; }
 
-template <int BN>
+template <int BN, int WM, int MI>
 static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, const uint16_t* wexp, const QWeight& w,
                        int m, int kchunk, void* out, int ldo, hipStream_t stream) {
-  constexpr int lds = f16_lds_bytes(BN);
+  constexpr int lds = f16_lds_bytes(32 * MI * WM, BN);
   auto launch = [&](auto kernel) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
       (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       configured = true;
     }
-    kernel<<<grid, 4 * BN / 128 * 64, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
+    kernel<<<grid, WM * BN / 128 * 64, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
   };
-  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN>);
-  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN>);
-  else launch(gemm_f16_kernel<kEpiSwiGLU, BN>);
+  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI>);
+  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI>);
+  else launch(gemm_f16_kernel<kEpiSwiGLU, BN, WM, MI>);
 }
 
 static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
-                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream, int bn) {
+                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream, int tile) {
+  const int bm = f16_bm(tile), bn = f16_bn(tile);
   if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
@@ -699,9 +724,14 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
   else if (w.type == kQ6_K) expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
   else expand_kernel<kQ4_0><<<blocks, 256, 0, stream>>>(w, wexp);
   const int kchunk = w.k / splits;
-  dim3 grid((w.n + bn - 1) / bn, (m + kBigBM - 1) / kBigBM, splits);
-  if (bn == 256) launch_f16<256>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream);
-  else launch_f16<128>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream);
+  dim3 grid((w.n + bn - 1) / bn, (m + bm - 1) / bm, splits);
+  switch (tile) {
+    case kF16T256x256: launch_f16<256, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T256x128: launch_f16<128, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T192x256: launch_f16<256, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T128x256: launch_f16<256, 2, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -714,8 +744,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
   if (forced < 0 && use_mid(w, m, splits)) forced = kVarMid;
-  const int bn = (wexp && forced < 0) ? two_pass_bn(w, m, splits) : 0;
-  if (bn) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, bn);
+  const int tile = (wexp && forced < 0) ? two_pass_tile(w, m, splits) : kF16None;
+  if (tile != kF16None) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile);
   const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
 #define NEMO_LAUNCH(T)                                                                                              \
   if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
@@ -750,8 +780,9 @@ hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, in
                                 uint16_t* wexp, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
   if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
-  const int bn = w.n % 256 == 0 ? 256 : 128;
-  return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream, bn);
+  int tile = two_pass_tile(w, m, 1);  // the plan's tile for this size, else the widest that fits
+  if (tile == kF16None) tile = w.n % 256 == 0 ? kF16T256x256 : kF16T256x128;
+  return launch_two_pass(x, ldx, w, m, kEpiStore, 1, y, ldy, wexp, stream, tile);
 }
 
 }  // namespace nemo

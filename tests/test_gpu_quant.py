@@ -145,7 +145,8 @@ def test_matmul_large_tiles_vs_oracle(torch_cuda, type_, m, n, k):
 
 
 @pytest.mark.parametrize("type_,m,n,k", [
-    (12, 2400, 16384, 2048),   # gate/up at 16 x 150 tokens
+    (12, 2400, 16384, 2048),   # gate/up at 16 x 150 tokens: 256 x 256 tiles
+    (12, 1536, 16384, 2048),   # after the merge: 192 x 256 tiles
     (14, 2400, 2048, 8192),    # down
     (12, 333, 200, 768),       # ragged rows and columns: clamped tile edges
     (14, 70, 384, 512),
