@@ -675,13 +675,14 @@ static int f16_bn(int t) { return t == kF16T256x128 ? 128 : 256; }
 
 // Tile of the two-pass GEMM for this problem, or kF16None when the fused
 // kernels are the better choice (measured on the encoder's shapes): 256 x 256
-// tiles once they alone give every CU a workgroup; 256 x 128 tiles for
-// unsplit problems with at least 64 of them (the QKV projection). Split-K
-// problems with fewer 256-column tiles do better on the fused 128-row tiles,
-// of which two or more fit on a CU.
+// tiles once they alone give every CU a workgroup (Q6_K, whose fused decode
+// costs more VALU work per weight: from 192 workgroups, the down projection
+// after the merge); 256 x 128 tiles for unsplit problems with at least 64 of
+// them (the QKV projection). Split-K problems with fewer 256-column tiles do
+// better on the fused 128-row tiles, of which two or more fit on a CU.
 static int two_pass_tile(const QWeight& w, int m, int splits) {
   const int mt = (m + kBigBM - 1) / kBigBM;
-  if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= 256) {
+  if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= (w.type == kQ6_K ? 192 : 256)) {
     // 192-row tiles (4 waves; measured at ~0.83 of the 256-row tiles' rate
     // per flop) when their rounds of 256 workgroups cost less: 1536 tokens
     // give 384 tiles of 256 rows (two rounds, the second half empty) but 512
