@@ -721,8 +721,12 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
   if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
-  if (w.type == kQ4_K) expand_kernel<kQ4_K><<<blocks, 256, 0, stream>>>(w, wexp);
-  else if (w.type == kQ6_K) expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
+  if (w.type == kQ4_K) {
+    // GGUF Q4_K rows are whole blocks: the row-major f16 matrix is the
+    // blocks' decode in order (full-line stores, same values).
+    const hipError_t e = launch_expand_q4k(w.blocks, (int64_t)w.n * (w.k / 256), wexp, stream);
+    if (e != hipSuccess) return e;
+  } else if (w.type == kQ6_K) expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
   else expand_kernel<kQ4_0><<<blocks, 256, 0, stream>>>(w, wexp);
   const int kchunk = w.k / splits;
   dim3 grid((w.n + bn - 1) / bn, (m + bm - 1) / bm, splits);

@@ -63,6 +63,9 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 // results are bit-identical to the fused kernels'.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
                           int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
+// Q4_K blocks -> f16, row-major (the two-pass GEMM's first pass for Q4_K).
+hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* out16, hipStream_t stream);
+
 // K-split count of the small-batch regime (17 <= m <= kSplitMaxM rows, one
 // 64-row tile): a function of the weight's shape only.
 int mid_splits(const QWeight& w);

@@ -329,40 +329,59 @@ hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
 // Standalone decoding.
 // ---------------------------------------------------------------------------
 
-// Q4_K raw: 8 threads per 144-byte block; thread c decodes nibble bytes
-// [16(c%2), +16) of group c/2: 16 low-nibble and 16 high-nibble values.
-__global__ void dequant_q4k_kernel(const uint8_t* __restrict__ raw, int64_t n_blocks, float* __restrict__ out32,
-                                   uint16_t* __restrict__ out16) {
+// Q4_K raw: 8 threads per 144-byte block. Thread c writes output chunks c,
+// c + 8, c + 16, c + 24 of 8 values (values 64 i + 8 c .. +8 for group i),
+// so each store instruction of 8 neighbouring lanes fills 128 contiguous
+// bytes (f16) or 256 (f32): the low nibbles of bytes 8c .. 8c + 8 of every
+// group's 32 (c < 4) or the high nibbles of bytes 8(c - 4) .. (c >= 4).
+// NT: non-temporal stores, for output that is not read back soon.
+template <bool NT>
+__global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restrict__ raw, int64_t n_blocks,
+                                                          float* __restrict__ out32, uint16_t* __restrict__ out16) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t b = t >> 3;
   if (b >= n_blocks) return;
-  const int c = (int)(t & 7), g = c >> 1, h = c & 1;
+  const int c = (int)(t & 7), part = c & 3, high = c >> 2;
   const uint8_t* blk = raw + b * 144;
   const u32x4 hdr = *(const u32x4*)blk;
-  const u32x4 q = *(const u32x4*)(blk + 16 + 32 * g + 16 * h);
-  float dsc0, ndm0, dsc1, ndm1;
-  q4k_group_factors(hdr, g, dsc0, ndm0, dsc1, ndm1);
-  const uint32_t words[4] = {q.x, q.y, q.z, q.w};
-  float vl[16], vh[16];
+  uint32_t q[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    bytes4_fma(words[i] & 0x0f0f0f0fu, dsc0, ndm0, vl + 4 * i);
-    bytes4_fma((words[i] >> 4) & 0x0f0f0f0fu, dsc1, ndm1, vh + 4 * i);
+    const uint2 w = *(const uint2*)(blk + 16 + 32 * i + 8 * part);
+    q[i][0] = w.x;
+    q[i][1] = w.y;
   }
-  const int64_t lo = b * 256 + 64 * g + 16 * h, hi = lo + 32;
-  if (out32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(float4v*)(out32 + lo + 4 * i) = float4v{vl[4 * i], vl[4 * i + 1], vl[4 * i + 2], vl[4 * i + 3]};
-      *(float4v*)(out32 + hi + 4 * i) = float4v{vh[4 * i], vh[4 * i + 1], vh[4 * i + 2], vh[4 * i + 3]};
+  for (int i = 0; i < 4; ++i) {
+    float dsc0, ndm0, dsc1, ndm1;
+    q4k_group_factors(hdr, i, dsc0, ndm0, dsc1, ndm1);
+    const float dsc = high ? dsc1 : dsc0, ndm = high ? ndm1 : ndm0;
+    const int sh = 4 * high;
+    float v[8];
+    bytes4_fma(opaque((q[i][0] >> sh) & 0x0f0f0f0fu), dsc, ndm, v);
+    bytes4_fma(opaque((q[i][1] >> sh) & 0x0f0f0f0fu), dsc, ndm, v + 4);
+    const int64_t o = b * 256 + 64 * i + 8 * c;
+    if constexpr (NT) {
+      if (out32) {
+        __builtin_nontemporal_store(float4v{v[0], v[1], v[2], v[3]}, (float4v*)(out32 + o));
+        __builtin_nontemporal_store(float4v{v[4], v[5], v[6], v[7]}, (float4v*)(out32 + o + 4));
+      }
+      if (out16) __builtin_nontemporal_store(to_half8(v), (half8v*)(out16 + o));
+    } else {
+      if (out32) {
+        *(float4v*)(out32 + o) = float4v{v[0], v[1], v[2], v[3]};
+        *(float4v*)(out32 + o + 4) = float4v{v[4], v[5], v[6], v[7]};
+      }
+      if (out16) *(half8v*)(out16 + o) = to_half8(v);
     }
   }
-  if (out16) {
-    *(half8v*)(out16 + lo) = to_half8(vl);
-    *(half8v*)(out16 + lo + 8) = to_half8(vl + 8);
-    *(half8v*)(out16 + hi) = to_half8(vh);
-    *(half8v*)(out16 + hi + 8) = to_half8(vh + 8);
-  }
+}
+
+hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* out16, hipStream_t stream) {
+  if (n_blocks <= 0) return hipSuccess;
+  dequant_q4k_kernel<false><<<(unsigned)((n_blocks * 8 + 255) / 256), 256, 0, stream>>>(blocks, n_blocks, nullptr,
+                                                                                        out16);
+  return hipGetLastError();
 }
 
 // Blocks whose size is not a multiple of 16 bytes (Q6_K 210, Q4_0 18) are
@@ -445,7 +464,7 @@ hipError_t launch_dequant_raw(int type, const uint8_t* raw, int64_t n_blocks, fl
   if (n_blocks <= 0) return hipSuccess;
   if (type == kQ4_K) {
     const int64_t threads = n_blocks * 8;
-    dequant_q4k_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(raw, n_blocks, out32, out16);
+    dequant_q4k_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(raw, n_blocks, out32, out16);
   } else if (type == kQ6_K) {
     dequant_q6k_kernel<<<(unsigned)((n_blocks + kQ6Span - 1) / kQ6Span), 256, 0, stream>>>(raw, n_blocks, out32, out16);
   } else if (type == kQ4_0) {
