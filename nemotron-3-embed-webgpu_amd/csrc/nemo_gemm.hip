@@ -726,8 +726,12 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
     // blocks' decode in order (full-line stores, same values).
     const hipError_t e = launch_expand_q4k(w.blocks, (int64_t)w.n * (w.k / 256), wexp, stream);
     if (e != hipSuccess) return e;
-  } else if (w.type == kQ6_K) expand_kernel<kQ6_K><<<blocks, 256, 0, stream>>>(w, wexp);
-  else expand_kernel<kQ4_0><<<blocks, 256, 0, stream>>>(w, wexp);
+  } else if (w.type == kQ6_K) {
+    const hipError_t e = launch_expand_q6k(w, wexp, stream);
+    if (e != hipSuccess) return e;
+  } else {
+    expand_kernel<kQ4_0><<<blocks, 256, 0, stream>>>(w, wexp);
+  }
   const int kchunk = w.k / splits;
   dim3 grid((w.n + bn - 1) / bn, (m + bm - 1) / bm, splits);
   switch (tile) {

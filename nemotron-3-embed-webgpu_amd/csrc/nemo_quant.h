@@ -65,6 +65,8 @@ hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
                           int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
 // Q4_K blocks -> f16, row-major (the two-pass GEMM's first pass for Q4_K).
 hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* out16, hipStream_t stream);
+// A Q6_K matrix (split layout) -> f16, row-major.
+hipError_t launch_expand_q6k(const QWeight& w, uint16_t* out16, hipStream_t stream);
 
 // K-split count of the small-batch regime (17 <= m <= kSplitMaxM rows, one
 // 64-row tile): a function of the weight's shape only.

@@ -475,6 +475,50 @@ hipError_t launch_dequant_raw(int type, const uint8_t* raw, int64_t n_blocks, fl
   return hipGetLastError();
 }
 
+// Q6_K split layout -> f16, row-major (the two-pass GEMM's first pass):
+// 8 threads per 256-value block, thread c writing chunks c + 8 i of 8
+// values, so 8 neighbouring lanes fill 128 contiguous bytes per store. Value
+// 64 i + 8 c + j is (half h = i / 2, quadrant Q = 2 (i % 2) + c / 4, lane
+// l = 8 (c % 4) + j) (src/gguf/quantization.ts:53-71): its low bits are the
+// low (Q < 2) or high nibble of ql[64 h + 8 c + j], its high bits bits 2Q of
+// qh[32 h + 8 (c % 4) + j], its scale sc[8 h + (c % 4) / 2 + 2 Q].
+__global__ __launch_bounds__(256) void expand_q6k_kernel(QWeight w, uint16_t* __restrict__ out16) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = t >> 3;
+  if (b >= (int64_t)w.n * (w.k >> 8)) return;
+  const int c = (int)(t & 7);
+  const uint8_t* rec = w.blocks + b * 208;
+  uint2 ql[2], qh[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    ql[h] = *(const uint2*)(rec + 64 * h + 8 * c);
+    qh[h] = *(const uint2*)(rec + 128 + 32 * h + 8 * (c & 3));
+  }
+  const u32x4 sc = *(const u32x4*)(rec + 192);
+  const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+  const float d = h2f(w.d[b]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = i >> 1, Q = 2 * (i & 1) + (c >> 2);
+    const int si = 8 * h + ((c & 3) >> 1) + 2 * Q;
+    const float dsc = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xffu);
+    const int ls = 4 * (i & 1), hs = 2 * Q;
+    const uint32_t w0 = ((ql[h].x >> ls) & 0x0f0f0f0fu) | (((qh[h].x >> hs) & 0x03030303u) << 4);
+    const uint32_t w1 = ((ql[h].y >> ls) & 0x0f0f0f0fu) | (((qh[h].y >> hs) & 0x03030303u) << 4);
+    float v[8];
+    bytes4_fma(opaque(w0), dsc, -32.0f * dsc, v);
+    bytes4_fma(opaque(w1), dsc, -32.0f * dsc, v + 4);
+    *(half8v*)(out16 + b * 256 + 64 * i + 8 * c) = to_half8(v);
+  }
+}
+
+hipError_t launch_expand_q6k(const QWeight& w, uint16_t* out16, hipStream_t stream) {
+  const int64_t threads = (int64_t)w.n * (w.k / 256) * 8;
+  if (threads <= 0) return hipSuccess;
+  expand_q6k_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(w, out16);
+  return hipGetLastError();
+}
+
 // Q6_K split layout -> float32: thread per (block, 32 values).
 __global__ void dequant_q6k_split_kernel(QWeight w, float* __restrict__ out32) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
