@@ -430,39 +430,53 @@ hipError_t launch_merge(const uint16_t* in, const Ragged& src, const Ragged& dst
 }
 
 // ---------------------------------------------------------------------------
-// Mean pool + L2 normalise (src/webgpu/ops.ts:596-615). One workgroup per
-// request; each thread owns 8 consecutive columns (16-byte loads per row).
+// Mean pool + L2 normalise (src/webgpu/ops.ts:596-615), in two kernels so a
+// long request is read by many CUs:
+//  * mean_pool_sum_kernel, grid (hidden / 64, batch): a workgroup owns 64
+//    columns of one request; thread (g, p) sums 8 columns (16-byte loads) of
+//    rows p, p + 32, ... in order, and the 32 row phases are added in phase
+//    order: a fixed order that depends only on the request's length. Writes
+//    the means.
+//  * l2_normalize_kernel, one workgroup per request: scales the means to unit
+//    length (no epsilon, as the reference).
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void mean_pool_kernel(const uint16_t* __restrict__ norm, Ragged rows, int hidden,
-                                                        float* __restrict__ out) {
-  __shared__ float scratch[16];
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(256) void mean_pool_sum_kernel(const uint16_t* __restrict__ norm, Ragged rows,
+                                                            int hidden, float* __restrict__ out) {
+  __shared__ float part[32][64];
+  const int b = blockIdx.y, c0 = blockIdx.x * 64;
   const int r0 = rows.start[b], n = rows.start[b + 1] - r0;
-  float sq = 0.f;
-  for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
-    float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < n; ++p) {
-      const half8v v = *(const half8v*)(norm + (size_t)(r0 + p) * hidden + c);
+  const int g = threadIdx.x & 7, p = threadIdx.x >> 3;
+  float total[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = p; r < n; r += 32) {
+    const half8v v = *(const half8v*)(norm + (size_t)(r0 + r) * hidden + c0 + 8 * g);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) total[e] += (float)v[e];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float mean = total[e] / (float)n;
-      out[(size_t)b * hidden + c + e] = mean;
-      sq += mean * mean;
-    }
+    for (int e = 0; e < 8; ++e) total[e] += (float)v[e];
   }
-  const float inv = 1.0f / sqrtf(block_sum(sq, scratch));
-  for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[(size_t)b * hidden + c + e] *= inv;
+  for (int e = 0; e < 8; ++e) part[p][8 * g + e] = total[e];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    float sum = part[0][threadIdx.x];
+    for (int q = 1; q < 32; ++q) sum += part[q][threadIdx.x];
+    out[(size_t)b * hidden + c0 + threadIdx.x] = sum / (float)n;
+  }
+}
+
+__global__ __launch_bounds__(256) void l2_normalize_kernel(float* __restrict__ out, int hidden) {
+  __shared__ float scratch[16];
+  float* v = out + (size_t)blockIdx.x * hidden;
+  float sq = 0.f;
+  for (int c = threadIdx.x; c < hidden; c += blockDim.x) sq += v[c] * v[c];
+  const float inv = 1.0f / sqrtf(block_sum(sq, scratch));
+  for (int c = threadIdx.x; c < hidden; c += blockDim.x) v[c] *= inv;
 }
 
 hipError_t launch_mean_pool(const uint16_t* norm, const Ragged& rows, int hidden, float* out, hipStream_t stream) {
   if (rows.count <= 0) return hipSuccess;
-  mean_pool_kernel<<<rows.count, 256, 0, stream>>>(norm, rows, hidden, out);
+  if (hidden % 64) return hipErrorInvalidValue;
+  mean_pool_sum_kernel<<<dim3(hidden / 64, rows.count), 256, 0, stream>>>(norm, rows, hidden, out);
+  l2_normalize_kernel<<<rows.count, 256, 0, stream>>>(out, hidden);
   return hipGetLastError();
 }
 
