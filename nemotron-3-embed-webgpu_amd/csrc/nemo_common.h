@@ -43,4 +43,9 @@ __device__ __forceinline__ int ragged_find(const Ragged& r, int t) {
   return b;
 }
 
+// s_waitcnt immediate waiting for at most `n` outstanding vector memory
+// operations (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
 }  // namespace nemo

@@ -12,23 +12,33 @@ namespace nemo {
 
 // ---------------------------------------------------------------------------
 // GEMV for m <= 16 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
-// 16 T weight rows (T = 2 or 4 tiles of 16) and 8 consecutive 256-value
+// 16 T weight rows (T = 1, 2 or 4 tiles of 16) and 8 consecutive 256-value
 // blocks of K: wave w takes block 8 * blockIdx.y + w of all T tiles. A wave
 // issues all of its loads before their first use (one memory round trip per
 // wave), each X fragment feeds the MFMAs of the T tiles, and the 8 waves'
-// sums are added in LDS in wave order (deterministic). The first T/2 tiles
-// are consecutive rows of the first half of a 128-row group and the last T/2
-// the rows 64 later, so with the gate/up rows interleaved per 128-row group
-// a workgroup holds gate and up rows of the same features and SwiGLU
-// completes in it. K beyond 2048 splits over blockIdx.y into fp32 partials
-// that the consumer sums in split order.
+// sums are added in LDS in wave order (deterministic). For T >= 2 the first
+// T/2 tiles are consecutive rows of the first half of a 128-row group and
+// the last T/2 the rows 64 later, so with the gate/up rows interleaved per
+// 128-row group a workgroup holds gate and up rows of the same features and
+// SwiGLU completes in it. K beyond 2048 splits over blockIdx.y into fp32
+// partials that the consumer sums in split order.
 //
 // MFMA operands: lane l supplies A = X[token l%16][8 consecutive k] and
 // B = W[row l%16][the same 8 k]. Lane group kq = l/16 owns four runs of 16
 // consecutive k in every block (the bytes it loads), two MFMAs per run.
+//
+// X reaches the MFMAs through LDS: a wave reads its 16 x 256 slice of X
+// with 8 loads of 1 KB (two whole 512-byte rows each, so every load reads 8
+// full cache lines; loading the fragments straight from global memory
+// touches 16 or more lines per load), writes it to LDS and reads its
+// fragments back with ds_read_b128. Row t's 16-byte chunk s sits in slot
+// s ^ t of the row, which spreads the 16 rows a fragment read touches over
+// distinct banks. The slice is the wave's own; its region later holds the
+// wave's sums for the cross-wave reduction.
 // ---------------------------------------------------------------------------
 
 constexpr int kGvWaves = 8;
+constexpr int kGvXSlice = 16 * 256 * 2;  // LDS bytes of a wave's X slice
 
 // Q4_K: the lane group loads nibble bytes [16kq, +16) (group kq/2) and
 // [64 + 16kq, +16) (group 2 + kq/2); runs: 0 = first chunk's low nibbles,
@@ -139,29 +149,47 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
                                         typename std::conditional<TYPE == kQ6_K, GvQ6K, GvQ40>::type>::type;
   // P 16-row tiles of gate-half rows and the P matching tiles 64 rows later;
   // 4 / P workgroups per 128-row group.
-  constexpr int P = kGvTiles / 2, G = 4 / P;
-  __shared__ float4v red[kGvWaves][kGvTiles][64];
+  // T >= 2: P = T / 2 tiles of a 128-row group's first half and the P tiles
+  // 64 rows later, G workgroups per group; T = 1 (not SwiGLU): 16 rows.
+  static_assert(kGvTiles >= 2 || MODE != kGvSwiGLU, "SwiGLU pairs gate and up tiles");
+  constexpr int P = kGvTiles >= 2 ? kGvTiles / 2 : 1, G = kGvTiles >= 2 ? 4 / P : 8;
+  static_assert(kGvTiles * 64 * 16 <= kGvXSlice, "a wave's sums fit in its X region");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kGvWaves * kGvXSlice];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kq = lane >> 4, c = lane & 15;
   const int N = w.n, nblocks = w.k >> 8;
-  const int n0 = 128 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G);
+  const int n0 = kGvTiles >= 2 ? 128 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G) : 16 * blockIdx.x;
   const int blk = kGvWaves * blockIdx.y + wave;
   const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
+  uint8_t* sx = smem + wave * kGvXSlice;
 
   float4v acc[kGvTiles];
 #pragma unroll
   for (int t = 0; t < kGvTiles; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
   if (blk < nblocks) {
+    // Load i: rows 2i, 2i + 1 of the slice; lane l takes slot l & 31 of row
+    // 2i + l / 32 (chunk (l & 31) ^ row). Registers, then LDS: the compiler
+    // orders the wave's own LDS write and reads.
+    half8v xs[8];
+    {
+      const int t0 = lane >> 5, s = lane & 31;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int t = 2 * i + t0;
+        xs[i] = *(const half8v*)(x + (size_t)min(t, M - 1) * ldx + 256 * blk + 8 * (s ^ t));
+      }
+    }
     Raw raw[kGvTiles];
 #pragma unroll
     for (int t = 0; t < kGvTiles; ++t) raw[t].load(w, row_bytes, min(n0 + 16 * (t % P) + 64 * (t / P) + c, N - 1), blk, kq);
-    const uint16_t* xr = x + (size_t)min(c, M - 1) * ldx + 256 * blk;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *(half8v*)(sx + 1024 * i + 16 * lane) = xs[i];
     half8v xa[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : TYPE == kQ6_K ? gv_q6k_run_k(kq, r) : gv_q40_run_k(kq, r);
-      xa[2 * r] = *(const half8v*)(xr + k);
-      xa[2 * r + 1] = *(const half8v*)(xr + k + 8);
+      xa[2 * r] = *(const half8v*)(sx + 512 * c + 16 * ((k >> 3) ^ c));
+      xa[2 * r + 1] = *(const half8v*)(sx + 512 * c + 16 * (((k >> 3) + 1) ^ c));
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -173,15 +201,17 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r + 1], f1, acc[t], 0, 0, 0);
       }
   }
+  // The wave's sums replace its X slice (its fragment reads came first).
+  float4v* red = (float4v*)smem;  // [wave][tile][lane] at wave * kGvXSlice
 #pragma unroll
-  for (int t = 0; t < kGvTiles; ++t) red[wave][t][lane] = acc[t];
+  for (int t = 0; t < kGvTiles; ++t) red[(wave * kGvXSlice / 16) + t * 64 + lane] = acc[t];
   __syncthreads();
 
   // D layout: lane l, register i -> token 4 (l / 16) + i, row l % 16 of the tile.
   auto tile_sum = [&](int t) {
-    float4v s = red[0][t][lane];
+    float4v s = red[t * 64 + lane];
 #pragma unroll
-    for (int v = 1; v < kGvWaves; ++v) s += red[v][t][lane];
+    for (int v = 1; v < kGvWaves; ++v) s += red[v * (kGvXSlice / 16) + t * 64 + lane];
     return s;
   };
   if constexpr (MODE == kGvSwiGLU) {
@@ -277,15 +307,18 @@ template <int TYPE, int MODE>
 static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
                                hipStream_t stream) {
   // 4 tiles per wave (X fragments reused 4 times) once that alone gives
-  // every CU a workgroup; else 2, which halves each wave's serial decode. A
-  // row's arithmetic is the same either way.
-  const int groups = (w.n + 127) / 128;
-  if (2 * groups * gemv_splits(w) < 256) {
-    dim3 grid(4 * ((w.n + 127) / 128), gemv_splits(w));
-    gemv_kernel<TYPE, MODE, 2><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  // every CU a workgroup; else 2 when that does (or for SwiGLU, whose gate
+  // and up tiles pair up); else 1, which spreads a small matrix over the
+  // most CUs (2048 x 2048: 128 workgroups, 1.2x faster than 64 of 2 tiles).
+  // A row's arithmetic is the same in every configuration.
+  const int groups = (w.n + 127) / 128, splits = gemv_splits(w);
+  if (2 * groups * splits >= 256) {
+    gemv_kernel<TYPE, MODE, 4><<<dim3(2 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  } else if (MODE == kGvSwiGLU || 4 * groups * splits >= 256) {
+    gemv_kernel<TYPE, MODE, 2><<<dim3(4 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
   } else {
-    dim3 grid(2 * ((w.n + 127) / 128), gemv_splits(w));
-    gemv_kernel<TYPE, MODE, 4><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    if constexpr (MODE != kGvSwiGLU)
+      gemv_kernel<TYPE, MODE, 1><<<dim3(8 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
   }
 }
 
