@@ -487,11 +487,6 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
   *(half8v*)(dst + 40) = hi[1];
 }
 
-// s_waitcnt immediate waiting for at most `n` outstanding vector memory
-// operations (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
-// left at their maxima).
-constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
-
 // gemm_f16_kernel<EPI, BN, WM, MI>: BM x BN x 64 tiles, BM = 32 MI WM, with
 // WM waves along M (32 MI rows each) x BN/128 along N (128 columns each).
 // LDS: two stages of the BM x 64 X tile and the BN x 64 W tile (128 bytes
@@ -688,8 +683,10 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     // give 384 tiles of 256 rows (two rounds, the second half empty) but 512
     // of 192 rows (two full rounds of tiles 3/4 the size). Time per round is
     // taken as tile area / rate: 0.75 / 0.83 = 0.904 of a 256-row round.
-    const int t256 = mt * (w.n / 256), t192 = ((m + 191) / 192) * (w.n / 256);
-    if (splits == 1 && 904 * ((t192 + 255) / 256) < 1000 * ((t256 + 255) / 256)) return kF16T192x256;
+    // The same count holds per K split (the down projection's 4 splits at
+    // 1536 tokens: 192 workgroups of 256 rows, 256 of 192).
+    const int t256 = mt * (w.n / 256) * splits, t192 = ((m + 191) / 192) * (w.n / 256) * splits;
+    if (904 * ((t192 + 255) / 256) < 1000 * ((t256 + 255) / 256)) return kF16T192x256;
     return kF16T256x256;
   }
   if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) return kF16T256x128;
