@@ -264,7 +264,11 @@ struct nemo_plan {
   int batch = 0, sequence = 0, merged = 0;
   hipStream_t stream = nullptr;
   std::mutex mu;
-  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, q, k, attn, delta, ffn, out, rope, partials, wexp;
+  DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, attn, delta, ffn, out, rope, partials, wexp;
+  // Rows of the last layer run (the attention's RoPE positions) and, made
+  // on request, its rotated query and key heads.
+  Ragged last_rows{};
+  DevPtr q, k;
   uint32_t* h_ids = nullptr;   // pinned staging
   float* h_out = nullptr;
   ~nemo_plan() {
@@ -653,7 +657,7 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->merged = merged_length(sequence);
     const size_t tf = (size_t)batch * sequence, tr = (size_t)batch * p->merged;
     const size_t H = d.hidden, QKV = (size_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
-    const size_t QW = (size_t)d.q_heads * d.head_dim, KW = (size_t)d.kv_heads * d.head_dim, F = d.intermediate;
+    const size_t QW = (size_t)d.q_heads * d.head_dim, F = d.intermediate;
     hip_check(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking), "hipStreamCreate");
     p->ids = dev_alloc(tf * 4, "token ids");
     p->x_full = dev_alloc(tf * H * 2, "full residual stream");
@@ -661,8 +665,6 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->x_red = dev_alloc(tr * H * 2, "merged residual stream");
     p->norm_red = dev_alloc(tr * H * 2, "merged normalized hidden state");
     p->qkv = dev_alloc(tf * QKV * 2, "query + key + value raw");
-    p->q = dev_alloc(tf * QW * 2, "query rope");
-    p->k = dev_alloc(tf * KW * 2, "key rope");
     p->attn = dev_alloc(tf * QW * 2, "attention");
     p->delta = dev_alloc(tf * H * 2, "residual delta");
     p->ffn = dev_alloc(tf * F * 2, "SwiGLU output");
@@ -752,8 +754,17 @@ nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, 
     else if (n == "x_merged") src = plan->x_red.get(), bytes = tr * H * 2;
     else if (n == "norm_merged") src = plan->norm_red.get(), bytes = tr * H * 2;
     else if (n == "qkv") src = plan->qkv.get(), bytes = tf * QKV * 2;
-    else if (n == "q") src = plan->q.get(), bytes = tf * QW * 2;
-    else if (n == "k") src = plan->k.get(), bytes = tf * KW * 2;
+    else if (n == "q" || n == "k") {
+      // RoPE of the last layer's query and key heads, as the attention applied it.
+      if (!plan->q) plan->q = dev_alloc(tf * QW * 2, "query rope");
+      if (!plan->k) plan->k = dev_alloc(tf * KW * 2, "key rope");
+      hip_check(launch_rope((const uint16_t*)plan->qkv.get(), (int)QKV, plan->last_rows, (const float*)plan->rope.get(),
+                            d.q_heads, d.kv_heads, d.head_dim, (uint16_t*)plan->q.get(), (uint16_t*)plan->k.get(),
+                            plan->stream),
+                "rope");
+      src = n == "q" ? plan->q.get() : plan->k.get();
+      bytes = tf * (n == "q" ? QW : KW) * 2;
+    }
     else if (n == "attention") src = plan->attn.get(), bytes = tf * QW * 2;
     else if (n == "delta") src = plan->delta.get(), bytes = tf * H * 2;
     else if (n == "ffn") src = plan->ffn.get(), bytes = tf * F * 2;
@@ -808,8 +819,6 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
   uint16_t* x_red = (uint16_t*)p->x_red.get();
   uint16_t* norm_red = (uint16_t*)p->norm_red.get();
   uint16_t* qkv = (uint16_t*)p->qkv.get();
-  uint16_t* q = (uint16_t*)p->q.get();
-  uint16_t* k = (uint16_t*)p->k.get();
   uint16_t* attn = (uint16_t*)p->attn.get();
   uint16_t* delta = (uint16_t*)p->delta.get();
   uint16_t* ffn = (uint16_t*)p->ffn.get();
@@ -866,9 +875,9 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     for (const auto& part : w.qkv_parts) qkv_proj(part.first, part.second);
     mark(2, false);
     mark(3, true);
-    hip_check(launch_rope(qkv, QKV, rows, rope, d.q_heads, d.kv_heads, d.head_dim, q, k, s), "rope");
-    hip_check(launch_attention(q, k, qkv + (size_t)(d.q_heads + d.kv_heads) * d.head_dim, QKV, rows, d.q_heads,
-                               d.kv_heads, d.head_dim, d.kv_stride_threshold, d.kv_stride, attn, s),
+    p->last_rows = rows;
+    hip_check(launch_attention(qkv, QKV, rope, rows, d.q_heads, d.kv_heads, d.head_dim, d.kv_stride_threshold,
+                               d.kv_stride, attn, s),
               "attention");
     mark(3, false);
     // Residual projection (O or down) then x += delta; RMSNorm. With a K

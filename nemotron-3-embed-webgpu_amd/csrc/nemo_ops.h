@@ -24,15 +24,18 @@ hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int split
                                    uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream);
 
 // Rotate adjacent pairs of the query and key heads of qkv into q [t, Hq, hd]
-// and k [t, Hkv, hd]; position = row index within its request.
+// and k [t, Hkv, hd]; position = row index within its request; table =
+// [position][pair] (cos, sin) floats. The attention applies the same
+// rotation itself; this writes it out.
 hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, const float* table, int q_heads,
                        int kv_heads, int head_dim, uint16_t* q, uint16_t* k, hipStream_t stream);
 
-// Bidirectional GQA attention per request; v rows are read from
-// v_base + t * v_stride + kv_head * head_dim.
-hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v_base, int v_stride,
-                            const Ragged& rows, int q_heads, int kv_heads, int head_dim, int stride_threshold,
-                            int key_stride, uint16_t* out, hipStream_t stream);
+// Bidirectional GQA attention per request on the QKV projection (row t:
+// Hq query heads, Hkv key heads, Hkv value heads), queries and keys rotated
+// by RoPE with `rope_table` as they are loaded.
+hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* rope_table, const Ragged& rows,
+                            int q_heads, int kv_heads, int head_dim, int stride_threshold, int key_stride, uint16_t* out,
+                            hipStream_t stream);
 
 // out[t, :F] = f16(silu(g) * u), g = gu[t, :F], u = gu[t, F:2F].
 hipError_t launch_swiglu(const uint16_t* gu, int rows, int f, uint16_t* out, hipStream_t stream);

@@ -162,8 +162,25 @@ hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int split
 
 // ---------------------------------------------------------------------------
 // Pairwise RoPE (src/webgpu/ops.ts:168-193): (e, o) -> (e c - o s, e s + o c)
-// with (c, s) = table[position][pair]. One workgroup per token.
+// with (c, s) = table[position][pair], on 8 consecutive values of a head (4
+// pairs) at a time. The attention kernel applies it as it loads queries and
+// keys from the QKV projection; rope_kernel writes the rotated heads out
+// (one workgroup per token) for inspection of the stage.
 // ---------------------------------------------------------------------------
+
+// v = values 2p0 .. 2p0 + 7 of a head; cs = table row + 2 p0 (c, s of 4 pairs).
+__device__ __forceinline__ half8v rope8(half8v v, const float* __restrict__ cs) {
+  const float4v a = *(const float4v*)cs, b = *(const float4v*)(cs + 4);
+  const float c[4] = {a[0], a[2], b[0], b[2]}, sn[4] = {a[1], a[3], b[1], b[3]};
+  half8v r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float e = (float)v[2 * j], o = (float)v[2 * j + 1];
+    r[2 * j] = (half_t)(e * c[j] - o * sn[j]);
+    r[2 * j + 1] = (half_t)(e * sn[j] + o * c[j]);
+  }
+  return r;
+}
 
 __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ qkv, int qkv_stride, Ragged rows,
                                                    const float* __restrict__ table, int q_heads, int kv_heads,
@@ -171,19 +188,15 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ 
   const int t = blockIdx.x;
   const int b = ragged_find(rows, t);
   const int pos = t - rows.start[b];
-  const int pairs = head_dim / 2;
-  const int total = (q_heads + kv_heads) * pairs;
-  const float* trow = table + (size_t)pos * pairs * 2;
+  const int chunks = head_dim / 8, total = (q_heads + kv_heads) * chunks;
+  const float* trow = table + (size_t)pos * head_dim;
   for (int i = threadIdx.x; i < total; i += blockDim.x) {
-    const int head = i / pairs, pair = i - head * pairs;
-    const uint32_t in = *(const uint32_t*)(qkv + (size_t)t * qkv_stride + head * head_dim + 2 * pair);
-    const float e = h2f((uint16_t)(in & 0xffffu)), o = h2f((uint16_t)(in >> 16));
-    const float c = trow[2 * pair], s = trow[2 * pair + 1];
-    const uint32_t outv = (uint32_t)f2h(e * c - o * s) | ((uint32_t)f2h(e * s + o * c) << 16);
+    const int head = i / chunks, d = 8 * (i - head * chunks);
+    const half8v r = rope8(*(const half8v*)(qkv + (size_t)t * qkv_stride + head * head_dim + d), trow + d);
     if (head < q_heads)
-      *(uint32_t*)(q + ((size_t)t * q_heads + head) * head_dim + 2 * pair) = outv;
+      *(half8v*)(q + ((size_t)t * q_heads + head) * head_dim + d) = r;
     else
-      *(uint32_t*)(k + ((size_t)t * kv_heads + (head - q_heads)) * head_dim + 2 * pair) = outv;
+      *(half8v*)(k + ((size_t)t * kv_heads + (head - q_heads)) * head_dim + d) = r;
   }
 }
 
@@ -191,13 +204,17 @@ hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, 
                        int kv_heads, int head_dim, uint16_t* q, uint16_t* k, hipStream_t stream) {
   const int total = rows.start[rows.count];
   if (total <= 0) return hipSuccess;
+  if (head_dim % 8) return hipErrorInvalidValue;
   rope_kernel<<<total, 256, 0, stream>>>(qkv, qkv_stride, rows, table, q_heads, kv_heads, head_dim, q, k);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // Bidirectional GQA flash attention on MFMA (src/webgpu/ops.ts:213-293,
-// 295-362). For request b with n valid rows, query i attends keys
+// 295-362), reading queries, keys and values from the QKV projection [t,
+// (Hq + 2 Hkv) hd] and rotating queries and keys (RoPE, position = row
+// within the request) as it loads them. For request b with n valid rows,
+// query i attends keys
 // 0, s, 2s, ... < n (s = key_stride if n > stride_threshold, else 1) with
 // scores q.k * head_dim^-1/2 * temperature(i), temperature = 1 + 0.1
 // ln(floor(i / 16384) + 1) for i >= 16384 (ops.ts:241); online softmax in
@@ -217,10 +234,10 @@ hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, 
 constexpr int kAttnQ = 32, kAttnKeys = 32, kVtPad = 40;
 
 template <int HD>
-__global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                                        const uint16_t* __restrict__ v_base, int v_stride,
-                                                        Ragged rows, int q_heads, int kv_heads, int stride_threshold,
-                                                        int key_stride_long, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
+                                                        const float* __restrict__ table, Ragged rows, int q_heads,
+                                                        int kv_heads, int stride_threshold, int key_stride_long,
+                                                        uint16_t* __restrict__ out) {
   constexpr int KP = HD + 8;  // padded K row (halves)
   constexpr int DC = HD / 16; // 16-wide d chunks of the score MFMAs
   constexpr int DB = HD / 32; // 32-wide d blocks of the output
@@ -248,10 +265,14 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
 
   half8v qf[DC];
   {
-    const uint16_t* qp = q + ((size_t)(row0 + min(qi, n - 1)) * q_heads + h) * HD + 8 * hl;
+    const int qpos = min(qi, n - 1);
+    const uint16_t* qp = qkv + (size_t)(row0 + qpos) * qkv_stride + h * HD + 8 * hl;
+    const float* cs = table + (size_t)qpos * HD + 8 * hl;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) qf[c] = *(const half8v*)(qp + 16 * c);
+    for (int c = 0; c < DC; ++c) qf[c] = rope8(*(const half8v*)(qp + 16 * c), cs + 16 * c);
   }
+  const uint16_t* kbase = qkv + (q_heads + kvh) * HD;
+  const uint16_t* vbase = qkv + (q_heads + kv_heads + kvh) * HD;
   float16v o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -263,14 +284,14 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
     __syncthreads();
     for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
       const int j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-      u32x4 kv4 = {0u, 0u, 0u, 0u};
-      half8v vv = {};
+      half8v kv = {}, vv = {};
       if (kb + j < n_keys) {
-        const int trow = row0 + (kb + j) * key_stride;
-        kv4 = *(const u32x4*)(k + ((size_t)trow * kv_heads + kvh) * HD + c);
-        vv = *(const half8v*)(v_base + (size_t)trow * v_stride + kvh * HD + c);
+        const int kpos = (kb + j) * key_stride;
+        const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
+        kv = rope8(*(const half8v*)(kbase + trow + c), table + (size_t)kpos * HD + c);
+        vv = *(const half8v*)(vbase + trow + c);
       }
-      *(u32x4*)&sK[j * KP + c] = kv4;
+      *(half8v*)&sK[j * KP + c] = kv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) sVt[(c + e) * kVtPad + j] = vv[e];
     }
@@ -337,9 +358,9 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
     }
 }
 
-hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v_base, int v_stride,
-                            const Ragged& rows, int q_heads, int kv_heads, int head_dim, int stride_threshold,
-                            int key_stride, uint16_t* out, hipStream_t stream) {
+hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* rope_table, const Ragged& rows,
+                            int q_heads, int kv_heads, int head_dim, int stride_threshold, int key_stride, uint16_t* out,
+                            hipStream_t stream) {
   int tiles = 0;
   for (int b = 0; b < rows.count; ++b) tiles += (rows.start[b + 1] - rows.start[b] + kAttnQ - 1) / kAttnQ;
   if (tiles == 0) return hipSuccess;
@@ -347,10 +368,10 @@ hipError_t launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t
   if (group < 1 || group > 8 || q_heads % kv_heads) return hipErrorInvalidValue;
   dim3 grid(tiles, kv_heads);
   if (head_dim == 64)
-    attention_kernel<64><<<grid, 64 * group, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads,
+    attention_kernel<64><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
                                                           stride_threshold, key_stride, out);
   else if (head_dim == 128)
-    attention_kernel<128><<<grid, 64 * group, 0, stream>>>(q, k, v_base, v_stride, rows, q_heads, kv_heads,
+    attention_kernel<128><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
                                                            stride_threshold, key_stride, out);
   else
     return hipErrorInvalidValue;
