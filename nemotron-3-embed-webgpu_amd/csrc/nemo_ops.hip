@@ -93,7 +93,12 @@ hipError_t launch_embed(const uint32_t* ids, int padded_seq, const Ragged& rows,
 // split order and rounded to f16 (the reference's delta buffer is f16).
 // ---------------------------------------------------------------------------
 
-template <bool PARTIALS>
+// DELTA = 0: normalize x; -1: x += f16 delta first; S >= 1: x += the sum of
+// S fp32 K-split partials first (all 2 S loads issued before the first add,
+// added in split order); kAnySplits: the same for a run-time count.
+constexpr int kAnySplits = 1000;
+
+template <int DELTA>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, const void* __restrict__ delta,
                                                       int splits, int rows, const float* __restrict__ w,
                                                       uint16_t* __restrict__ out, int hidden, float eps) {
@@ -102,15 +107,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, 
   float sum = 0.f;
   for (int c = threadIdx.x * 8; c < hidden; c += blockDim.x * 8) {
     half8v xv = *(const half8v*)(x + base + c);
-    if (delta) {
+    if constexpr (DELTA != 0) {
       float dv[8];
-      if constexpr (PARTIALS) {
+      if constexpr (DELTA > 0) {
         const float* p = (const float*)delta + base + c;
-        float4v a = *(const float4v*)p, b = *(const float4v*)(p + 4);
-        for (int s = 1; s < splits; ++s) {
-          const float* q = p + (size_t)s * rows * hidden;
-          a += *(const float4v*)q;
-          b += *(const float4v*)(q + 4);
+        const size_t slice = (size_t)rows * hidden;
+        float4v a, b;
+        if constexpr (DELTA == kAnySplits) {
+          a = *(const float4v*)p, b = *(const float4v*)(p + 4);
+          for (int s = 1; s < splits; ++s) {
+            a += *(const float4v*)(p + s * slice);
+            b += *(const float4v*)(p + s * slice + 4);
+          }
+        } else {
+          float4v pa[DELTA], pb[DELTA];
+#pragma unroll
+          for (int s = 0; s < DELTA; ++s) {
+            pa[s] = *(const float4v*)(p + s * slice);
+            pb[s] = *(const float4v*)(p + s * slice + 4);
+          }
+          a = pa[0], b = pb[0];
+#pragma unroll
+          for (int s = 1; s < DELTA; ++s) a += pa[s], b += pb[s];
         }
         const float raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
@@ -149,14 +167,30 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, 
 hipError_t launch_rmsnorm(uint16_t* x, const uint16_t* delta, const float* w, uint16_t* normalized, int rows,
                           int hidden, float eps, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
-  rmsnorm_kernel<false><<<rows, 256, 0, stream>>>(x, delta, 1, rows, w, normalized, hidden, eps);
+  if (delta)
+    rmsnorm_kernel<-1><<<rows, 256, 0, stream>>>(x, delta, 1, rows, w, normalized, hidden, eps);
+  else
+    rmsnorm_kernel<0><<<rows, 256, 0, stream>>>(x, nullptr, 1, rows, w, normalized, hidden, eps);
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int splits, const float* w,
                                    uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
-  rmsnorm_kernel<true><<<rows, 256, 0, stream>>>(x, partials, splits, rows, w, normalized, hidden, eps);
+  if (splits < 1) return hipErrorInvalidValue;
+#define NEMO_NORM(S) rmsnorm_kernel<S><<<rows, 256, 0, stream>>>(x, partials, splits, rows, w, normalized, hidden, eps)
+  switch (splits) {
+    case 1: NEMO_NORM(1); break;
+    case 2: NEMO_NORM(2); break;
+    case 3: NEMO_NORM(3); break;
+    case 4: NEMO_NORM(4); break;
+    case 6: NEMO_NORM(6); break;
+    case 8: NEMO_NORM(8); break;
+    case 12: NEMO_NORM(12); break;
+    case 16: NEMO_NORM(16); break;
+    default: NEMO_NORM(kAnySplits); break;
+  }
+#undef NEMO_NORM
   return hipGetLastError();
 }
 
