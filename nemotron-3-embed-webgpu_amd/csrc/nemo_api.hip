@@ -5,6 +5,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -269,6 +270,10 @@ struct nemo_plan {
   // on request, its rotated query and key heads.
   Ragged last_rows{};
   DevPtr q, k;
+  // Rotated attended keys and transposed values of a pass's long requests
+  // (attention's preparation pass), room for attn_keys_cap keys per kv head.
+  DevPtr attn_ks, attn_vts;
+  int attn_keys_cap = 0;
   uint32_t* h_ids = nullptr;   // pinned staging
   float* h_out = nullptr;
   ~nemo_plan() {
@@ -666,6 +671,12 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->norm_red = dev_alloc(tr * H * 2, "merged normalized hidden state");
     p->qkv = dev_alloc(tf * QKV * 2, "query + key + value raw");
     p->attn = dev_alloc(tf * QW * 2, "attention");
+    if (sequence >= kAttnPrepRows) {
+      p->attn_keys_cap = batch * ((sequence + 31) / 32 * 32);
+      const size_t halves = (size_t)d.kv_heads * p->attn_keys_cap * d.head_dim;
+      p->attn_ks = dev_alloc(halves * 2, "attention keys");
+      p->attn_vts = dev_alloc(halves * 2, "attention values (transposed)");
+    }
     p->delta = dev_alloc(tf * H * 2, "residual delta");
     p->ffn = dev_alloc(tf * F * 2, "SwiGLU output");
     // fp32 split-K partial sums of the projections that split K.
@@ -876,8 +887,14 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     mark(2, false);
     mark(3, true);
     p->last_rows = rows;
+    // Requests of kAttnPrepRows rows or more: keys rotated and values
+    // transposed once per layer instead of once per 32-query tile.
+    int longest = 0;
+    for (int b = 0; b < rows.count; ++b) longest = std::max(longest, rows.start[b + 1] - rows.start[b]);
+    const bool prep = p->attn_ks && longest >= kAttnPrepRows;
     hip_check(launch_attention(qkv, QKV, rope, rows, d.q_heads, d.kv_heads, d.head_dim, d.kv_stride_threshold,
-                               d.kv_stride, attn, s),
+                               d.kv_stride, attn, s, prep ? (uint16_t*)p->attn_ks.get() : nullptr,
+                               prep ? (uint16_t*)p->attn_vts.get() : nullptr, p->attn_keys_cap),
               "attention");
     mark(3, false);
     // Residual projection (O or down) then x += delta; RMSNorm. With a K

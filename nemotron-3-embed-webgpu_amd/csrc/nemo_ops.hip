@@ -267,22 +267,79 @@ hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, 
 
 constexpr int kAttnQ = 32, kAttnKeys = 32, kVtPad = 40;
 
+__device__ __forceinline__ int attn_keys(int n, int stride_threshold, int key_stride_long) {
+  const int s = n > stride_threshold ? key_stride_long : 1;
+  return (n + s - 1) / s;
+}
+
+// Long requests: one pass per layer writes each request's attended keys,
+// rotated, as K_s [kv head][key][hd] and its values transposed as
+// V^T_s [kv head][hd][key] (keys of request b from 32 * (sum over earlier
+// requests of ceil(keys / 32)), zero past the last key). The attention's
+// query tiles (157 of them at 5000 tokens) then stage both with 16-byte
+// loads and stores instead of rotating every key again and transposing V
+// with 2-byte LDS stores. Workgroup = 32 keys of one kv head.
 template <int HD>
+__global__ __launch_bounds__(256) void attention_prep_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
+                                                             const float* __restrict__ table, Ragged rows,
+                                                             int q_heads, int kv_heads, int stride_threshold,
+                                                             int key_stride_long, int keys_cap,
+                                                             uint16_t* __restrict__ ks, uint16_t* __restrict__ vts) {
+  __shared__ __attribute__((aligned(16))) half_t sv[kAttnKeys * (HD + 8)];
+  int b = 0, blk = blockIdx.x;
+  for (; b < rows.count; ++b) {
+    const int blocks = (attn_keys(rows.start[b + 1] - rows.start[b], stride_threshold, key_stride_long) + 31) / 32;
+    if (blk < blocks) break;
+    blk -= blocks;
+  }
+  if (b >= rows.count) return;
+  const int row0 = rows.start[b], n = rows.start[b + 1] - row0;
+  const int key_stride = n > stride_threshold ? key_stride_long : 1;
+  const int n_keys = (n + key_stride - 1) / key_stride;
+  const int kvh = blockIdx.y, g0 = kAttnKeys * blockIdx.x;  // first key of this block in the buffers
+  const uint16_t* kbase = qkv + (q_heads + kvh) * HD;
+  const uint16_t* vbase = qkv + (q_heads + kv_heads + kvh) * HD;
+  for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
+    const int j = i / (HD / 8), c = (i % (HD / 8)) * 8, key = kAttnKeys * blk + j;
+    half8v kv = {}, vv = {};
+    if (key < n_keys) {
+      const int kpos = key * key_stride;
+      const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
+      kv = rope8(*(const half8v*)(kbase + trow + c), table + (size_t)kpos * HD + c);
+      vv = *(const half8v*)(vbase + trow + c);
+    }
+    *(half8v*)(ks + ((size_t)kvh * keys_cap + g0 + j) * HD + c) = kv;
+    *(half8v*)&sv[j * (HD + 8) + c] = vv;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < HD * kAttnKeys / 8; i += blockDim.x) {
+    const int d = i / (kAttnKeys / 8), k0 = (i % (kAttnKeys / 8)) * 8;
+    half8v col;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) col[r] = sv[(k0 + r) * (HD + 8) + d];
+    *(half8v*)(vts + ((size_t)kvh * HD + d) * keys_cap + g0 + k0) = col;
+  }
+}
+
+template <int HD, bool PREP>
 __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
                                                         const float* __restrict__ table, Ragged rows, int q_heads,
                                                         int kv_heads, int stride_threshold, int key_stride_long,
+                                                        const uint16_t* __restrict__ ks,
+                                                        const uint16_t* __restrict__ vts, int keys_cap,
                                                         uint16_t* __restrict__ out) {
   constexpr int KP = HD + 8;  // padded K row (halves)
   constexpr int DC = HD / 16; // 16-wide d chunks of the score MFMAs
   constexpr int DB = HD / 32; // 32-wide d blocks of the output
   __shared__ __attribute__((aligned(16))) half_t sK[kAttnKeys * KP];
   __shared__ __attribute__((aligned(16))) half_t sVt[HD * kVtPad];
-  int b = 0, tile = blockIdx.x;
+  int b = 0, tile = blockIdx.x, koff = 0;  // koff: the request's first key in K_s / V^T_s
   for (; b < rows.count; ++b) {
     const int n = rows.start[b + 1] - rows.start[b];
     const int tiles = (n + kAttnQ - 1) / kAttnQ;
     if (tile < tiles) break;
     tile -= tiles;
+    koff += kAttnKeys * ((attn_keys(n, stride_threshold, key_stride_long) + kAttnKeys - 1) / kAttnKeys);
   }
   if (b >= rows.count) return;
   const int row0 = rows.start[b];
@@ -316,18 +373,28 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
 
   for (int kb = 0; kb < n_keys; kb += kAttnKeys) {
     __syncthreads();
-    for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
-      const int j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-      half8v kv = {}, vv = {};
-      if (kb + j < n_keys) {
-        const int kpos = (kb + j) * key_stride;
-        const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
-        kv = rope8(*(const half8v*)(kbase + trow + c), table + (size_t)kpos * HD + c);
-        vv = *(const half8v*)(vbase + trow + c);
+    if constexpr (PREP) {
+      const uint16_t* kp = ks + ((size_t)kvh * keys_cap + koff + kb) * HD;
+      for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x)
+        *(half8v*)&sK[(i / (HD / 8)) * KP + (i % (HD / 8)) * 8] = *(const half8v*)(kp + 8 * i);
+      for (int i = threadIdx.x; i < HD * kAttnKeys / 8; i += blockDim.x) {
+        const int d = i / (kAttnKeys / 8), k0 = (i % (kAttnKeys / 8)) * 8;
+        *(half8v*)&sVt[d * kVtPad + k0] = *(const half8v*)(vts + ((size_t)kvh * HD + d) * keys_cap + koff + kb + k0);
       }
-      *(half8v*)&sK[j * KP + c] = kv;
+    } else {
+      for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
+        const int j = i / (HD / 8), c = (i % (HD / 8)) * 8;
+        half8v kv = {}, vv = {};
+        if (kb + j < n_keys) {
+          const int kpos = (kb + j) * key_stride;
+          const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
+          kv = rope8(*(const half8v*)(kbase + trow + c), table + (size_t)kpos * HD + c);
+          vv = *(const half8v*)(vbase + trow + c);
+        }
+        *(half8v*)&sK[j * KP + c] = kv;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sVt[(c + e) * kVtPad + j] = vv[e];
+        for (int e = 0; e < 8; ++e) sVt[(c + e) * kVtPad + j] = vv[e];
+      }
     }
     __syncthreads();
     // S^T block: lane holds query l%32, key kb + 8(r/4) + 4hl + r%4.
@@ -392,23 +459,47 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
     }
 }
 
+int attention_prep_keys(const Ragged& rows, int stride_threshold, int key_stride) {
+  int keys = 0;
+  for (int b = 0; b < rows.count; ++b) {
+    const int n = rows.start[b + 1] - rows.start[b];
+    const int s = n > stride_threshold ? key_stride : 1;
+    keys += kAttnKeys * (((n + s - 1) / s + kAttnKeys - 1) / kAttnKeys);
+  }
+  return keys;
+}
+
 hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* rope_table, const Ragged& rows,
                             int q_heads, int kv_heads, int head_dim, int stride_threshold, int key_stride, uint16_t* out,
-                            hipStream_t stream) {
+                            hipStream_t stream, uint16_t* ks, uint16_t* vts, int keys_cap) {
   int tiles = 0;
   for (int b = 0; b < rows.count; ++b) tiles += (rows.start[b + 1] - rows.start[b] + kAttnQ - 1) / kAttnQ;
   if (tiles == 0) return hipSuccess;
   const int group = q_heads / kv_heads;
   if (group < 1 || group > 8 || q_heads % kv_heads) return hipErrorInvalidValue;
+  if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
+  const bool prep = ks != nullptr;
+  if (prep) {
+    const int keys = attention_prep_keys(rows, stride_threshold, key_stride);
+    if (!vts || keys > keys_cap) return hipErrorInvalidValue;
+    dim3 pgrid(keys / kAttnKeys, kv_heads);
+    if (head_dim == 64)
+      attention_prep_kernel<64><<<pgrid, 256, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
+                                                           stride_threshold, key_stride, keys_cap, ks, vts);
+    else
+      attention_prep_kernel<128><<<pgrid, 256, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
+                                                            stride_threshold, key_stride, keys_cap, ks, vts);
+  }
   dim3 grid(tiles, kv_heads);
-  if (head_dim == 64)
-    attention_kernel<64><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
-                                                          stride_threshold, key_stride, out);
-  else if (head_dim == 128)
-    attention_kernel<128><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads,
-                                                           stride_threshold, key_stride, out);
-  else
-    return hipErrorInvalidValue;
+#define NEMO_ATTN(HD, P)                                                                                          \
+  attention_kernel<HD, P><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads, \
+                                                           stride_threshold, key_stride, ks, vts, keys_cap, out)
+  if (head_dim == 64) {
+    if (prep) NEMO_ATTN(64, true); else NEMO_ATTN(64, false);
+  } else {
+    if (prep) NEMO_ATTN(128, true); else NEMO_ATTN(128, false);
+  }
+#undef NEMO_ATTN
   return hipGetLastError();
 }
 

@@ -77,6 +77,27 @@ def test_forward_matches_oracle(torch_cuda, cfg):
             assert _cos(single, oracle.forward_request(om, np.array(s))) >= 0.9999
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_long_requests_prepared_keys_match_oracle(torch_cuda, hd):
+    """A pass holding a request of 512 rows or more rotates the attended keys
+    and transposes the values once (the attention's preparation pass) instead
+    of once per query tile: ragged long and short requests, stride-3 keys for
+    those longer than 400, both layers before the merge."""
+    Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
+    dims = rt.make_dims(hidden=256, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=512, layers=2, vocab=300,
+                        merge_after_layer=2, kv_stride_threshold=400)
+    tensors = synth.model_tensors(dims, seed=707 + hd, embedding_type=1)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    lengths = [700, 30, 520, 450, 1]
+    seqs = [[1] + list(synth.randint(1300 + i, n - 1, 2, 300)) for i, n in enumerate(lengths)]
+    ids, lens = _padded(seqs, 700)
+    got = model.createPlan(len(seqs), 700).run_sync(ids, lens)
+    for i, s in enumerate(seqs):
+        c = _cos(got[i], oracle.forward_request(om, np.array(s)))
+        assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
+
+
 def test_small_batches_take_the_gemv_and_stay_batch_invariant(torch_cuda):
     """Passes of at most 16 tokens run every projection on the split-K GEMV
     (its split count depends only on the weight): results match the oracle
