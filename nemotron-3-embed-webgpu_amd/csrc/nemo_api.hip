@@ -76,6 +76,7 @@ struct DevTensor {
   std::vector<int64_t> dims;
   DevPtr data;   // raw bytes (Q6_K: 208-byte records)
   DevPtr d6;     // Q6_K / Q4_0 matrices: per-block f16 scale (null when stored raw)
+  DevPtr gv;     // Q4_K matrices: the GEMV's tiled copy of the blocks (launch_tile_q4k)
   size_t bytes = 0;  // GGUF byte size
   // Gate/up rows reordered per 128-row tile (64 gate rows, then the matching
   // 64 up rows) for the GEMM's SwiGLU epilogue.
@@ -209,7 +210,18 @@ QWeight as_qweight(const DevTensor& t) {
   w.n = (int)t.dims[1];
   w.blocks = (const uint8_t*)t.data.get();
   w.d = (const uint16_t*)t.d6.get();
+  w.gv = (const uint8_t*)t.gv.get();
   return w;
+}
+
+// The GEMV's tiled copy of a Q4_K matrix with a multiple of 16 rows (also
+// 0.5625 bytes per weight); other matrices are read in place.
+void add_gemv_tiles(DevTensor& t) {
+  if (t.type != kQ4_K || t.dims.size() != 2 || t.dims[1] % 16 || t.gv) return;
+  t.gv = dev_alloc(t.bytes, "GEMV tiles");
+  hip_check(launch_tile_q4k((const uint8_t*)t.data.get(), (int)t.dims[1], (int)t.dims[0], (uint8_t*)t.gv.get(), 0),
+            "GEMV tiles");
+  hip_check(hipStreamSynchronize(0), "GEMV tiles");  // plans run on non-blocking streams
 }
 
 int merged_length(int sequence) {  // contextualMergedLength, src/webgpu/model.ts:30-32
@@ -492,13 +504,15 @@ static void fuse_rows(nemo_model* m, const std::string& name, const std::vector<
 }
 
 static QWeight matrix(nemo_model* m, const std::string& name, int64_t k, int64_t n) {
-  const DevTensor& t = need(m, name);
+  need(m, name);
+  DevTensor& t = m->tensors[name];
   if (t.dims.size() != 2) fail(NEMO_ERR_INVALID, "invalid matrix " + name);
   if (t.type != kQ4_K && t.type != kQ6_K && t.type != kQ4_0)
     fail(NEMO_ERR_UNSUPPORTED, "unsupported matrix type " + std::to_string(t.type) + " for " + name);
   if (t.dims[0] != k || t.dims[1] != n)
     fail(NEMO_ERR_INVALID, name + " has dims [" + std::to_string(t.dims[0]) + ", " + std::to_string(t.dims[1]) +
                                "]; expected [" + std::to_string(k) + ", " + std::to_string(n) + "]");
+  add_gemv_tiles(t);
   return as_qweight(t);
 }
 
@@ -541,7 +555,9 @@ nemo_status nemo_model_finalize(nemo_model* model) {
       if (!gu.gate_up_interleaved) {
         interleave_gate_up(gu, F);
         gu.gate_up_interleaved = true;
+        gu.gv.reset();  // tiles of the interleaved rows
       }
+      add_gemv_tiles(gu);
       layers[l].gate_up = as_qweight(gu);
       layers[l].down = matrix(model, p + "ffn_down.weight", F, H);
       layers[l].attn_norm = vec_f32(model, p + "attn_norm.weight", H);
@@ -1051,6 +1067,7 @@ nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int3
     auto w = std::make_unique<nemo_weight>();
     w->ctx = ctx;
     upload_tensor(w->t, ggml_type, {k, n}, bytes, n_bytes, "weight");
+    add_gemv_tiles(w->t);
     w->w = as_qweight(w->t);
     const size_t pf = gemv_partials_floats(w->w, 16);
     if (pf) w->partials = dev_alloc(pf * 4, "GEMV partials");
