@@ -214,13 +214,15 @@ QWeight as_qweight(const DevTensor& t) {
   return w;
 }
 
-// The GEMV's tiled copy of a Q4_K matrix with a multiple of 16 rows (also
-// 0.5625 bytes per weight); other matrices are read in place.
+// The GEMV's tiled copy of a Q4_K, Q6_K or Q4_0 matrix with a multiple of
+// 16 rows (as many bytes as the matrix); other matrices are read in place.
 void add_gemv_tiles(DevTensor& t) {
-  if (t.type != kQ4_K || t.dims.size() != 2 || t.dims[1] % 16 || t.gv) return;
-  t.gv = dev_alloc(t.bytes, "GEMV tiles");
-  hip_check(launch_tile_q4k((const uint8_t*)t.data.get(), (int)t.dims[1], (int)t.dims[0], (uint8_t*)t.gv.get(), 0),
-            "GEMV tiles");
+  if (t.dims.size() != 2 || t.gv) return;
+  const QWeight w = as_qweight(t);
+  const size_t bytes = (t.type == kQ4_K || t.type == kQ6_K || t.type == kQ4_0) ? gemv_tile_bytes(w) : 0;
+  if (!bytes || (t.type != kQ4_K && !t.d6)) return;
+  t.gv = dev_alloc(bytes, "GEMV tiles");
+  hip_check(launch_tile_gemv(w, (uint8_t*)t.gv.get(), 0), "GEMV tiles");
   hip_check(hipStreamSynchronize(0), "GEMV tiles");  // plans run on non-blocking streams
 }
 

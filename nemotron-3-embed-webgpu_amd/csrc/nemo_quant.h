@@ -26,8 +26,8 @@ struct QWeight {
   int k;
   const uint8_t* blocks;
   const uint16_t* d;
-  // Q4_K only, optional: the same blocks regrouped for the GEMV (see
-  // launch_tile_q4k); null when absent.
+  // Optional: the same blocks regrouped for the GEMV (launch_tile_gemv);
+  // null when absent.
   const uint8_t* gv = nullptr;
 };
 
@@ -66,12 +66,13 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 // results are bit-identical to the fused kernels'.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
                           int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
-// Q4_K rows regrouped for the GEMV (n % 16 == 0, `out` the same size as the
-// blocks): per 16-row tile and 256-value block, 2304 bytes holding the 16
-// rows' 16-byte headers, then the first 64 nibble bytes of each row as
-// [16-byte part][row], then the last 64 likewise, so each of a GEMV wave's
-// three loads per tile reads whole contiguous lines.
-hipError_t launch_tile_q4k(const uint8_t* blocks, int n, int k, uint8_t* out, hipStream_t stream);
+// A matrix's blocks regrouped for the GEMV (n % 16 == 0): per 16-row tile
+// and 256 values, the bytes each lane group of a GEMV wave loads sit
+// side by side for the 16 rows, so every load of the wave reads whole
+// contiguous lines (loading from the row-major blocks touches 16 lines per
+// load). gemv_tile_bytes: the copy's size (0: the matrix has no tiled form).
+size_t gemv_tile_bytes(const QWeight& w);
+hipError_t launch_tile_gemv(const QWeight& w, uint8_t* out, hipStream_t stream);
 // Q4_K blocks -> f16, row-major (the two-pass GEMM's first pass for Q4_K).
 hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* out16, hipStream_t stream);
 // A Q6_K matrix (split layout) -> f16, row-major.

@@ -97,6 +97,19 @@ struct GvQ6K {
     sc = *(const u32x4*)(rec + 192);
     d = w.d[(size_t)row * (w.k >> 8) + blk];
   }
+  // From the tiled copy (launch_tile_gemv): 3360 bytes per 16-row tile and
+  // block: ql first halves [kq][row], ql second halves, qh first halves
+  // [half][row], qh second halves, the 16 scale bytes [row], d [row].
+  __device__ __forceinline__ void load_tiled(const QWeight& w, int tile, int c, int blk, int kq) {
+    const uint8_t* base = w.gv + ((size_t)tile * (w.k >> 8) + blk) * 3360;
+    const int h = kq >> 1;
+    ql0 = *(const u32x4*)(base + 16 * (16 * kq + c));
+    ql1 = *(const u32x4*)(base + 1024 + 16 * (16 * kq + c));
+    qh0 = *(const u32x4*)(base + 2048 + 16 * (16 * h + c));
+    qh1 = *(const u32x4*)(base + 2560 + 16 * (16 * h + c));
+    sc = *(const u32x4*)(base + 3072 + 16 * c);
+    d = *(const uint16_t*)(base + 3328 + 2 * c);
+  }
   __device__ __forceinline__ void run(int kq, int r, half8v& f0, half8v& f1) const {
     const int h = kq >> 1, Q = (kq & 1) + 2 * (r >> 1), jh = r & 1;
     const u32x4 ql = jh ? ql1 : ql0, qh = jh ? qh1 : qh0;
@@ -133,6 +146,17 @@ struct GvQ40 {
     const uint16_t* d = w.d + (size_t)row * (w.k >> 5) + b;
     d0 = d[0];
     d1 = d[1];
+  }
+  // From the tiled copy (launch_tile_gemv): 2304 bytes per 16-row tile and
+  // 256 values: first blocks of the pairs [kq][row], second blocks, the two
+  // scales [kq][row].
+  __device__ __forceinline__ void load_tiled(const QWeight& w, int tile, int c, int blk, int kq) {
+    const uint8_t* base = w.gv + ((size_t)tile * (w.k >> 8) + blk) * 2304;
+    q0 = *(const u32x4*)(base + 16 * (16 * kq + c));
+    q1 = *(const u32x4*)(base + 1024 + 16 * (16 * kq + c));
+    const uint32_t dd = *(const uint32_t*)(base + 2048 + 4 * (16 * kq + c));
+    d0 = (uint16_t)(dd & 0xffffu);
+    d1 = (uint16_t)(dd >> 16);
   }
   __device__ __forceinline__ void run(int kq, int r, half8v& f0, half8v& f1) const {
     const u32x4 q = (r >> 1) ? q1 : q0;
@@ -319,20 +343,17 @@ template <int TYPE, int MODE>
 static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
                                hipStream_t stream) {
   const int groups = (w.n + 127) / 128, splits = gemv_splits(w);
-  if constexpr (TYPE == kQ4_K) {
-    if (w.gv && w.n % 16 == 0) {
-      // Tiled Q4_K: 2 tiles per wave when that gives every CU a workgroup
-      // (or for SwiGLU), else 1 (measured: 16384 x 2048 7.7 us on 2 tiles,
-      // 7.9 on 4; 2048 x 2048 3.7 us on 1 against 4.5 untiled).
-      if (MODE == kGvSwiGLU || 4 * groups * splits >= 256) {
-        gemv_kernel<TYPE, MODE, 2, true><<<dim3(4 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
-      } else {
-        if constexpr (MODE != kGvSwiGLU)
-          gemv_kernel<TYPE, MODE, 1, true><<<dim3(8 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out,
-                                                                                                     ldo);
-      }
-      return;
+  if (w.gv && w.n % 16 == 0) {
+    // Tiled weights: 2 tiles per wave when that gives every CU a workgroup
+    // (or for SwiGLU), else 1 (measured on Q4_K: 16384 x 2048 7.7 us on 2
+    // tiles, 7.9 on 4; 2048 x 2048 3.7 us on 1 against 4.5 untiled).
+    if (MODE == kGvSwiGLU || 4 * groups * splits >= 256) {
+      gemv_kernel<TYPE, MODE, 2, true><<<dim3(4 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    } else {
+      if constexpr (MODE != kGvSwiGLU)
+        gemv_kernel<TYPE, MODE, 1, true><<<dim3(8 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
     }
+    return;
   }
   // 4 tiles per wave (X fragments reused 4 times) once that alone gives
   // every CU a workgroup; else 2 when that does (or for SwiGLU, whose gate
@@ -349,9 +370,10 @@ static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int
   }
 }
 
-// One thread per 16-byte piece p of row r, block b: p = 0 the header, 1-4
-// the first 64 nibble bytes, 5-8 the last 64.
+// Tiled copies for the GEMV (one thread per piece of row r, 256-value block
+// b; layouts at the load_tiled functions above).
 __global__ void tile_q4k_kernel(const uint8_t* __restrict__ src, int n, int nblocks, uint8_t* __restrict__ dst) {
+  // piece p: 0 the header, 1-4 the first 64 nibble bytes, 5-8 the last 64
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)n * nblocks * 9) return;
   const int p = (int)(i % 9);
@@ -363,10 +385,70 @@ __global__ void tile_q4k_kernel(const uint8_t* __restrict__ src, int n, int nblo
   *(u32x4*)o = v;
 }
 
-hipError_t launch_tile_q4k(const uint8_t* blocks, int n, int k, uint8_t* out, hipStream_t stream) {
-  if (n <= 0 || n % 16 || k <= 0 || k % 256) return hipErrorInvalidValue;
-  const int64_t pieces = (int64_t)n * (k / 256) * 9;
-  tile_q4k_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, stream>>>(blocks, n, k / 256, out);
+__global__ void tile_q6k_kernel(const uint8_t* __restrict__ rec, const uint16_t* __restrict__ dsrc, int n,
+                                int nblocks, uint8_t* __restrict__ dst) {
+  // piece p: 0-7 ql (16 bytes each), 8-11 qh, 12 the scales, 13 d
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)n * nblocks * 14) return;
+  const int p = (int)(i % 14);
+  const int64_t rb = i / 14;
+  const int b = (int)(rb % nblocks), r = (int)(rb / nblocks), c = r & 15;
+  const uint8_t* src = rec + ((size_t)r * nblocks + b) * 208;
+  uint8_t* base = dst + ((size_t)(r >> 4) * nblocks + b) * 3360;
+  if (p == 13) {
+    *(uint16_t*)(base + 3328 + 2 * c) = dsrc[(size_t)r * nblocks + b];
+    return;
+  }
+  const u32x4 v = *(const u32x4*)(src + 16 * p);
+  uint8_t* o;
+  if (p < 8) {  // ql bytes 16p: kq = p / 2 (h = kq / 2, qa = kq % 2), second half when p is odd
+    o = base + (p & 1) * 1024 + 16 * (16 * (p >> 1) + c);
+  } else if (p < 12) {  // qh bytes 128 + 16 (p - 8): half (p - 8) / 2, second half when p is odd
+    o = base + 2048 + (p & 1) * 512 + 16 * (16 * ((p - 8) >> 1) + c);
+  } else {
+    o = base + 3072 + 16 * c;
+  }
+  *(u32x4*)o = v;
+}
+
+__global__ void tile_q40_kernel(const uint8_t* __restrict__ nib, const uint16_t* __restrict__ dsrc, int n,
+                                int nblocks, uint8_t* __restrict__ dst) {
+  // piece p of a 256-value block: 0-7 the eight 16-byte nibble blocks, 8-11 the scale pairs
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)n * nblocks * 12) return;
+  const int p = (int)(i % 12);
+  const int64_t rb = i / 12;
+  const int b = (int)(rb % nblocks), r = (int)(rb / nblocks), c = r & 15;
+  uint8_t* base = dst + ((size_t)(r >> 4) * nblocks + b) * 2304;
+  if (p < 8) {  // Q4_0 block 8b + p: pair kq = p / 2, second of the pair when p is odd
+    const u32x4 v = *(const u32x4*)(nib + ((size_t)r * nblocks * 8 + 8 * b + p) * 16);
+    *(u32x4*)(base + (p & 1) * 1024 + 16 * (16 * (p >> 1) + c)) = v;
+  } else {
+    const int kq = p - 8;
+    const uint16_t* d = dsrc + (size_t)r * nblocks * 8 + 8 * b + 2 * kq;
+    *(uint32_t*)(base + 2048 + 4 * (16 * kq + c)) = (uint32_t)d[0] | ((uint32_t)d[1] << 16);
+  }
+}
+
+size_t gemv_tile_bytes(const QWeight& w) {
+  if (w.n <= 0 || w.n % 16 || w.k <= 0 || w.k % 256) return 0;
+  const size_t tiles = (size_t)(w.n / 16) * (w.k / 256);
+  return w.type == kQ4_K ? tiles * 2304 : w.type == kQ6_K ? tiles * 3360 : w.type == kQ4_0 ? tiles * 2304 : 0;
+}
+
+hipError_t launch_tile_gemv(const QWeight& w, uint8_t* out, hipStream_t stream) {
+  if (!gemv_tile_bytes(w)) return hipErrorInvalidValue;
+  const int nb = w.k / 256;
+  const int64_t rows_blocks = (int64_t)w.n * nb;
+  if (w.type == kQ4_K) {
+    tile_q4k_kernel<<<(unsigned)((rows_blocks * 9 + 255) / 256), 256, 0, stream>>>(w.blocks, w.n, nb, out);
+  } else if (w.type == kQ6_K) {
+    if (!w.d) return hipErrorInvalidValue;
+    tile_q6k_kernel<<<(unsigned)((rows_blocks * 14 + 255) / 256), 256, 0, stream>>>(w.blocks, w.d, w.n, nb, out);
+  } else {
+    if (!w.d) return hipErrorInvalidValue;
+    tile_q40_kernel<<<(unsigned)((rows_blocks * 12 + 255) / 256), 256, 0, stream>>>(w.blocks, w.d, w.n, nb, out);
+  }
   return hipGetLastError();
 }
 
