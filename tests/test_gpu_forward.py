@@ -98,6 +98,23 @@ def test_long_requests_prepared_keys_match_oracle(torch_cuda, hd):
         assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
 
 
+def test_request_past_16384_tokens_matches_oracle(torch_cuda):
+    """17,000 tokens: queries at positions >= 16384 scale their scores by the
+    temperature 1 + 0.1 ln(floor(i / 16384) + 1) (src/webgpu/ops.ts:241),
+    keys are sampled every third state and prepared once, and the merge
+    keeps 10,880 states."""
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, layers=1, vocab=300,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=1717, embedding_type=1)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    n = 17000
+    seq = np.concatenate([[1], synth.randint(1718, n - 1, 2, 300)])
+    got = model.createPlan(1, n).run_sync(seq.astype(np.uint32), [n])[0]
+    c = _cos(got, oracle.forward_request(om, seq))
+    assert c >= 0.9999, f"cosine {c:.6f}"
+
+
 def test_small_batches_take_the_gemv_and_stay_batch_invariant(torch_cuda):
     """Passes of at most 16 tokens run every projection on the split-K GEMV
     (its split count depends only on the weight): results match the oracle
