@@ -4,6 +4,8 @@
 //
 // Semantics follow src/webgpu/ops.ts (cited per kernel). Storage is f16 as in
 // the reference's buffers; arithmetic is fp32.
+#include <algorithm>
+
 #include "nemo_blocks.h"
 #include "nemo_common.h"
 #include "nemo_ops.h"
@@ -202,9 +204,9 @@ hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int split
 // (one workgroup per token) for inspection of the stage.
 // ---------------------------------------------------------------------------
 
-// v = values 2p0 .. 2p0 + 7 of a head; cs = table row + 2 p0 (c, s of 4 pairs).
-__device__ __forceinline__ half8v rope8(half8v v, const float* __restrict__ cs) {
-  const float4v a = *(const float4v*)cs, b = *(const float4v*)(cs + 4);
+// v = values 2p0 .. 2p0 + 7 of a head; (a, b) = the table's (c, s) of its 4
+// pairs (table row + 2 p0, 8 floats).
+__device__ __forceinline__ half8v rope8(half8v v, float4v a, float4v b) {
   const float c[4] = {a[0], a[2], b[0], b[2]}, sn[4] = {a[1], a[3], b[1], b[3]};
   half8v r;
 #pragma unroll
@@ -214,6 +216,9 @@ __device__ __forceinline__ half8v rope8(half8v v, const float* __restrict__ cs) 
     r[2 * j + 1] = (half_t)(e * sn[j] + o * c[j]);
   }
   return r;
+}
+__device__ __forceinline__ half8v rope8(half8v v, const float* __restrict__ cs) {
+  return rope8(v, *(const float4v*)cs, *(const float4v*)(cs + 4));
 }
 
 __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* __restrict__ qkv, int qkv_stride, Ragged rows,
@@ -326,13 +331,17 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
                                                         const float* __restrict__ table, Ragged rows, int q_heads,
                                                         int kv_heads, int stride_threshold, int key_stride_long,
                                                         const uint16_t* __restrict__ ks,
-                                                        const uint16_t* __restrict__ vts, int keys_cap,
+                                                        const uint16_t* __restrict__ vts, int keys_cap, int sb_keys,
                                                         uint16_t* __restrict__ out) {
   constexpr int KP = HD + 8;  // padded K row (halves)
   constexpr int DC = HD / 16; // 16-wide d chunks of the score MFMAs
   constexpr int DB = HD / 32; // 32-wide d blocks of the output
-  __shared__ __attribute__((aligned(16))) half_t sK[kAttnKeys * KP];
-  __shared__ __attribute__((aligned(16))) half_t sVt[HD * kVtPad];
+  // sb_keys (a multiple of 32) keys are staged per round: sK [sb_keys][KP],
+  // sVt [HD][VP].
+  extern __shared__ __attribute__((aligned(16))) uint8_t attn_lds[];
+  const int VP = sb_keys + 8;
+  half_t* sK = (half_t*)attn_lds;
+  half_t* sVt = sK + sb_keys * KP;
   int b = 0, tile = blockIdx.x, koff = 0;  // koff: the request's first key in K_s / V^T_s
   for (; b < rows.count; ++b) {
     const int n = rows.start[b + 1] - rows.start[b];
@@ -371,46 +380,70 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  for (int kb = 0; kb < n_keys; kb += kAttnKeys) {
+  for (int sb = 0; sb < n_keys; sb += sb_keys) {
+    const int staged = min(sb_keys, n_keys - sb);
     __syncthreads();
     if constexpr (PREP) {
-      const uint16_t* kp = ks + ((size_t)kvh * keys_cap + koff + kb) * HD;
-      for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x)
+      const uint16_t* kp = ks + ((size_t)kvh * keys_cap + koff + sb) * HD;
+      const int kch = (staged + 31) / 32 * 32 * HD / 8;  // whole 32-key blocks (zero-padded in K_s)
+      for (int i = threadIdx.x; i < kch; i += blockDim.x)
         *(half8v*)&sK[(i / (HD / 8)) * KP + (i % (HD / 8)) * 8] = *(const half8v*)(kp + 8 * i);
-      for (int i = threadIdx.x; i < HD * kAttnKeys / 8; i += blockDim.x) {
-        const int d = i / (kAttnKeys / 8), k0 = (i % (kAttnKeys / 8)) * 8;
-        *(half8v*)&sVt[d * kVtPad + k0] = *(const half8v*)(vts + ((size_t)kvh * HD + d) * keys_cap + koff + kb + k0);
+      const int vch = (staged + 31) / 32 * 4;  // 8-key chunks of a V^T row
+      for (int i = threadIdx.x; i < HD * vch; i += blockDim.x) {
+        const int d = i / vch, k0 = (i % vch) * 8;
+        *(half8v*)&sVt[d * VP + k0] = *(const half8v*)(vts + ((size_t)kvh * HD + d) * keys_cap + koff + sb + k0);
       }
     } else {
-      for (int i = threadIdx.x; i < kAttnKeys * HD / 8; i += blockDim.x) {
-        const int j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-        half8v kv = {}, vv = {};
-        if (kb + j < n_keys) {
-          const int kpos = (kb + j) * key_stride;
-          const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
-          kv = rope8(*(const half8v*)(kbase + trow + c), table + (size_t)kpos * HD + c);
-          vv = *(const half8v*)(vbase + trow + c);
-        }
-        *(half8v*)&sK[j * KP + c] = kv;
+      // 16-byte chunks of the staged keys (rows past `staged` up to the
+      // next multiple of 32 are zero), in batches of 4 per thread with every
+      // load of a batch issued before the first is used.
+      const int chunks = (staged + 31) / 32 * 32 * HD / 8;
+      for (int i0 = threadIdx.x; i0 < chunks; i0 += 4 * blockDim.x) {
+        half8v kr[4], vr[4];
+        float4v ca[4], cb[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sVt[(c + e) * kVtPad + j] = vv[e];
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
+          kr[u] = half8v{};
+          vr[u] = half8v{};
+          ca[u] = cb[u] = float4v{0.f, 0.f, 0.f, 0.f};
+          if (i < chunks && j < staged) {
+            const int kpos = (sb + j) * key_stride;
+            const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
+            kr[u] = *(const half8v*)(kbase + trow + c);
+            vr[u] = *(const half8v*)(vbase + trow + c);
+            const float* cs = table + (size_t)kpos * HD + c;
+            ca[u] = *(const float4v*)cs;
+            cb[u] = *(const float4v*)(cs + 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
+          if (i < chunks) {
+            *(half8v*)&sK[j * KP + c] = rope8(kr[u], ca[u], cb[u]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sVt[(c + e) * VP + j] = vr[u][e];
+          }
+        }
       }
     }
     __syncthreads();
+  for (int kb = 0; kb < staged; kb += kAttnKeys) {
     // S^T block: lane holds query l%32, key kb + 8(r/4) + 4hl + r%4.
     float16v s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      const half8v a = *(const half8v*)&sK[(lane & 31) * KP + 16 * c + 8 * hl];
+      const half8v a = *(const half8v*)&sK[(kb + (lane & 31)) * KP + 16 * c + 8 * hl];
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
     }
     float bm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-      s[r] = key < n_keys ? s[r] * scale2 : -INFINITY;
+      s[r] = key < staged ? s[r] * scale2 : -INFINITY;
       bm = fmaxf(bm, s[r]);
     }
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
@@ -437,13 +470,14 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
       const half8v pb = to_half8(p + 8 * c2);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const half_t* vr = &sVt[(32 * db + (lane & 31)) * kVtPad + 16 * c2 + 4 * hl];
+        const half_t* vr = &sVt[(32 * db + (lane & 31)) * VP + kb + 16 * c2 + 4 * hl];
         const half4v v0 = *(const half4v*)vr;
         const half4v v1 = *(const half4v*)(vr + 8);
         const half8v a = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[db], 0, 0, 0);
       }
     }
+  }
   }
   if (qi >= n) return;
   const float inv = 1.0f / lsum;
@@ -491,13 +525,35 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
                                                             stride_threshold, key_stride, keys_cap, ks, vts);
   }
   dim3 grid(tiles, kv_heads);
-#define NEMO_ATTN(HD, P)                                                                                          \
-  attention_kernel<HD, P><<<grid, 64 * group, 0, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads, \
-                                                           stride_threshold, key_stride, ks, vts, keys_cap, out)
+  // Keys staged per round: every key of the pass's longest request when
+  // they fit in ~72 KB of LDS and short requests only (one round of loads
+  // and barriers instead of one per 32 keys); 32 for the prepared path.
+  int longest_keys = 0;
+  for (int b = 0; b < rows.count; ++b) {
+    const int n = rows.start[b + 1] - rows.start[b];
+    const int s = n > stride_threshold ? key_stride : 1;
+    longest_keys = std::max(longest_keys, (n + s - 1) / s);
+  }
+  const int cap = 16384 / head_dim;  // 256 keys at head_dim 64, 128 at 128
+  const int sb = prep ? kAttnKeys : std::min(cap, (longest_keys + kAttnKeys - 1) / kAttnKeys * kAttnKeys);
+  const int lds = 2 * (sb * (head_dim + 8) + head_dim * (sb + 8));
+#define NEMO_ATTN(HD, P)                                                                                           \
+  attention_kernel<HD, P><<<grid, 64 * group, lds, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads, \
+                                                             stride_threshold, key_stride, ks, vts, keys_cap, sb, out)
+  auto attr = [&](const void* kernel) {
+    static bool configured[4] = {false, false, false, false};  // one attribute call per instantiation
+    const int slot = (head_dim == 64 ? 0 : 2) + (prep ? 1 : 0);
+    if (!configured[slot]) {
+      (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * (cap * (head_dim + 8) + head_dim * (cap + 8)));
+      configured[slot] = true;
+    }
+  };
   if (head_dim == 64) {
-    if (prep) NEMO_ATTN(64, true); else NEMO_ATTN(64, false);
+    if (prep) { attr((const void*)attention_kernel<64, true>); NEMO_ATTN(64, true); }
+    else { attr((const void*)attention_kernel<64, false>); NEMO_ATTN(64, false); }
   } else {
-    if (prep) NEMO_ATTN(128, true); else NEMO_ATTN(128, false);
+    if (prep) { attr((const void*)attention_kernel<128, true>); NEMO_ATTN(128, true); }
+    else { attr((const void*)attention_kernel<128, false>); NEMO_ATTN(128, false); }
   }
 #undef NEMO_ATTN
   return hipGetLastError();
