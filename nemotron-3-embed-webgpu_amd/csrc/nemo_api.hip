@@ -714,20 +714,8 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
         if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
       }
     }
-    // Passes of 17 to kSplitMaxM tokens split K further on the 64-row tiles.
-    if (tf > 16) {
-      const size_t split_m = std::min<size_t>(tf, kSplitMaxM);
-      for (const LayerWeights& w : model->layers) {
-        std::vector<const QWeight*> mats = qkv_matrices(w);
-        mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
-        for (const QWeight* q : mats) {
-          const int sp = mid_splits(*q);
-          if (sp > 1) partial_floats = std::max(partial_floats, (size_t)sp * split_m * q->n);
-        }
-      }
-    }
-    // Passes of at most 16 tokens take the GEMV, whose split counts differ.
-    const size_t small_m = std::min<size_t>(tf, 16);
+    // Passes of at most kGemvMaxM tokens take the GEMV, whose split counts differ.
+    const size_t small_m = std::min<size_t>(tf, kGemvMaxM);
     for (const LayerWeights& w : model->layers) {
       std::vector<const QWeight*> mats = qkv_matrices(w);
       mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
@@ -874,25 +862,17 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     uint16_t* norm = full ? norm_full : norm_red;
     const LayerWeights& w = m->layers[l];
     mark(2, true);
-    // At most 16 tokens: the split-K GEMV (HBM-bound; the MFMA tiles would
-    // leave most CUs idle). Up to kSplitMaxM tokens (one 64-row tile): K
-    // split into mid_splits chunks, reduced in chunk order. Each regime's
-    // split counts depend on the weight's shape only, so within a regime a
-    // token's result does not depend on the rest of the batch.
-    const bool small = M <= 16;
-    const bool split_mid = !small && M <= kSplitMaxM;
+    // At most kGemvMaxM tokens: the split-K GEMV (HBM-bound; the MFMA tiles
+    // would leave most CUs idle). Each regime's split counts depend on the
+    // weight's shape only, and the GEMV's arithmetic per token does not
+    // depend on the pass size, so within a regime a token's result does not
+    // depend on the rest of the batch.
+    const bool small = M <= kGemvMaxM;
     // One matrix, or separate q / k / v parts each into its column range.
     auto qkv_proj = [&](const QWeight& wq, int col) {
-      const int sp = split_mid ? mid_splits(wq) : gemm_splits(wq);
+      const int sp = gemm_splits(wq);
       if (small) {
         hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
-      } else if (split_mid) {
-        if (sp == 1) {
-          hip_check(launch_gemm_mid(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s), "qkv matmul");
-        } else {
-          hip_check(launch_gemm_mid(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s), "qkv matmul");
-          hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
-        }
       } else if (sp == 1) {
         hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp), "qkv matmul");
       } else {
@@ -918,16 +898,12 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
     auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
-      const int splits = small ? gemv_splits(wt) : split_mid ? mid_splits(wt) : gemm_splits(wt);
+      const int splits = small ? gemv_splits(wt) : gemm_splits(wt);
       mark(stage, true);
       if (small)
         hip_check(launch_gemv_ex(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial,
                                  splits == 1 ? (void*)delta : (void*)partials, H, nullptr, s),
                   "residual gemv");
-      else if (split_mid)
-        hip_check(launch_gemm_mid(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial, splits,
-                                  splits == 1 ? (void*)delta : (void*)partials, H, s),
-                  "residual matmul");
       else if (splits == 1)
         hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wexp), "residual matmul");
       else
@@ -944,14 +920,6 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
     if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
-    } else if (split_mid) {
-      const int sp = mid_splits(w.gate_up);
-      if (sp == 1) {
-        hip_check(launch_gemm_mid(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s), "gate/up matmul");
-      } else {
-        hip_check(launch_gemm_mid(norm, H, w.gate_up, M, kEpiPartial, sp, partials, w.gate_up.n, s), "gate/up matmul");
-        hip_check(launch_reduce_swiglu(partials, sp, M, w.gate_up.n, ffn, F, s), "gate/up reduce");
-      }
     } else {
       hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     }
@@ -1071,7 +1039,7 @@ nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int3
     upload_tensor(w->t, ggml_type, {k, n}, bytes, n_bytes, "weight");
     add_gemv_tiles(w->t);
     w->w = as_qweight(w->t);
-    const size_t pf = gemv_partials_floats(w->w, 16);
+    const size_t pf = gemv_partials_floats(w->w, kGemvMaxM);
     if (pf) w->partials = dev_alloc(pf * 4, "GEMV partials");
     *out = w.release();
   });
@@ -1095,11 +1063,11 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
     hipStream_t s = (hipStream_t)stream;
     if (algo < 0 || algo > 5) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
     const QWeight& w = weight->w;
-    const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= 16);
+    const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= kGemvMaxM);
     const bool two_pass =
         algo == NEMO_MATMUL_TWO_PASS || (algo == NEMO_MATMUL_AUTO && !gemv && gemm_two_pass(w, m, 1));
     if (gemv) {
-      if (m > 16) fail(NEMO_ERR_INVALID, "GEMV takes m <= 16");
+      if (m > kGemvMaxM) fail(NEMO_ERR_INVALID, "GEMV takes m <= " + std::to_string(kGemvMaxM));
       hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)weight->partials.get(), s), "gemv");
     } else if (algo == NEMO_MATMUL_GEMM_MID) {
       hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");

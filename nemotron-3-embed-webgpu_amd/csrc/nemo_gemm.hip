@@ -718,7 +718,9 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
   return kF16None;
 }
 
-bool gemm_two_pass(const QWeight& w, int m, int splits) { return two_pass_tile(w, m, splits) != kF16None; }
+bool gemm_two_pass(const QWeight& w, int m, int splits) {
+  return !use_mid(w, m, splits) && two_pass_tile(w, m, splits) != kF16None;
+}
 
 template <int BN, int WM, int MI>
 static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, const uint16_t* wexp, const QWeight& w,

@@ -78,10 +78,10 @@ hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* 
 // A Q6_K matrix (split layout) -> f16, row-major.
 hipError_t launch_expand_q6k(const QWeight& w, uint16_t* out16, hipStream_t stream);
 
-// K-split count of the small-batch regime (17 <= m <= kSplitMaxM rows, one
-// 64-row tile): a function of the weight's shape only.
+// K-split count of the 64-row split tiles (NEMO_MATMUL_GEMM_SPLIT): chunks
+// of at least 512 columns, enough for ~512 workgroups; a function of the
+// weight's shape only.
 int mid_splits(const QWeight& w);
-constexpr int kSplitMaxM = 64;
 
 // launch_gemm_ex on the 64-row deep-prefetch tiles whatever the size
 // (bit-identical to the other fused kernels).
@@ -96,16 +96,18 @@ hipError_t launch_reduce_partials(const float* partials, int splits, int m, int 
 hipError_t launch_reduce_swiglu(const float* partials, int splits, int m, int n, uint16_t* y, int ldy,
                                 hipStream_t stream);
 
-// Small-M path (m <= 16): MFMA GEMV, 64 rows x 2048 K per workgroup with an
-// in-workgroup reduction; K beyond 2048 splits into fp32 partials summed in
+// Small-M path (m <= kGemvMaxM): MFMA GEMV, 64 rows x 2048 K per workgroup
+// with an in-workgroup reduction, every decoded weight fragment applied to up
+// to 8 groups of 16 tokens; K beyond 2048 splits into fp32 partials summed in
 // split order through `partials` (float, at least gemv_partials_floats()).
+constexpr int kGemvMaxM = 128;
 size_t gemv_partials_floats(const QWeight& w, int m);
 // The GEMV's K-split count: a function of the weight's shape only.
 int gemv_splits(const QWeight& w);
 hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y, int ldy, int m,
                        float* partials, hipStream_t stream);
 
-// The GEMV with the GEMM's epilogues (m <= 16): kEpiStore as launch_gemv;
+// The GEMV with the GEMM's epilogues (m <= kGemvMaxM): kEpiStore as launch_gemv;
 // kEpiPartial writes [gemv_splits(w)][m][n] fp32 sums to `out` (ldo == n);
 // kEpiSwiGLU sums into `partials` (room for gemv_splits(w) * m * n floats),
 // then applies SwiGLU over the 128-row interleaved gate/up columns.

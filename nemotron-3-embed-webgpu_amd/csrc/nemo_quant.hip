@@ -1,5 +1,5 @@
 // Quantized-weight kernels for gfx950 besides the GEMM: the split-K
-// wavefront GEMV (m <= 16), GGML Q4_K / Q6_K / Q4_0 block decoding to
+// wavefront GEMV (m <= 128), GGML Q4_K / Q6_K / Q4_0 block decoding to
 // float32/f16 (bit-exact with src/gguf/quantization.ts:19-74), and the
 // fixed-order reduction of split-K partial sums.
 #include <type_traits>
@@ -11,12 +11,15 @@
 namespace nemo {
 
 // ---------------------------------------------------------------------------
-// GEMV for m <= 16 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
+// GEMV for m <= 128 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
 // 16 T weight rows (T = 1, 2 or 4 tiles of 16) and 8 consecutive 256-value
 // blocks of K: wave w takes block 8 * blockIdx.y + w of all T tiles. A wave
-// issues all of its loads before their first use (one memory round trip per
-// wave), each X fragment feeds the MFMAs of the T tiles, and the 8 waves'
-// sums are added in LDS in wave order (deterministic). For T >= 2 the first
+// issues all of its weight loads before their first use (one memory round
+// trip per wave) and decodes them once into MFMA fragments that serve every
+// group of 16 tokens in turn (the next group's X loads in flight meanwhile);
+// each X fragment feeds the MFMAs of the T tiles, and the 8 waves' sums are
+// added in LDS in wave order (deterministic). A token's arithmetic does not
+// depend on how many groups share the launch. For T >= 2 the first
 // T/2 tiles are consecutive rows of the first half of a 128-row group and
 // the last T/2 the rows 64 later, so with the gate/up rows interleaved per
 // 128-row group a workgroup holds gate and up rows of the same features and
@@ -173,18 +176,17 @@ struct GvQ40 {
 
 enum GvMode { kGvStore = 0, kGvPartial = 1, kGvSwiGLU = 2 };
 
-template <int TYPE, int MODE, int kGvTiles, bool TILED = false>
+template <int TYPE, int MODE, int kGvTiles, bool TILED = false, int NG = 1>
 __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __restrict__ x, int ldx, QWeight w, int M,
                                                              void* __restrict__ out, int ldo) {
   using Raw = typename std::conditional<TYPE == kQ4_K, GvQ4K,
                                         typename std::conditional<TYPE == kQ6_K, GvQ6K, GvQ40>::type>::type;
-  // P 16-row tiles of gate-half rows and the P matching tiles 64 rows later;
-  // 4 / P workgroups per 128-row group.
   // T >= 2: P = T / 2 tiles of a 128-row group's first half and the P tiles
   // 64 rows later, G workgroups per group; T = 1 (not SwiGLU): 16 rows.
+  // NG groups of 16 tokens (M <= 16 NG) share each decoded weight fragment.
   static_assert(kGvTiles >= 2 || MODE != kGvSwiGLU, "SwiGLU pairs gate and up tiles");
   constexpr int P = kGvTiles >= 2 ? kGvTiles / 2 : 1, G = kGvTiles >= 2 ? 4 / P : 8;
-  static_assert(kGvTiles * 64 * 16 <= kGvXSlice, "a wave's sums fit in its X region");
+  static_assert(kGvWaves * 64 * 16 <= kGvXSlice, "a round's sums of a wave fit in its X region");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kGvWaves * kGvXSlice];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kq = lane >> 4, c = lane & 15;
@@ -194,22 +196,26 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
   const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
   uint8_t* sx = smem + wave * kGvXSlice;
 
-  float4v acc[kGvTiles];
+  float4v acc[NG][kGvTiles];
 #pragma unroll
-  for (int t = 0; t < kGvTiles; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int t = 0; t < kGvTiles; ++t) acc[g][t] = float4v{0.f, 0.f, 0.f, 0.f};
   if (blk < nblocks) {
-    // Load i: rows 2i, 2i + 1 of the slice; lane l takes slot l & 31 of row
-    // 2i + l / 32 (chunk (l & 31) ^ row). Registers, then LDS: the compiler
-    // orders the wave's own LDS write and reads.
+    // Load i of token group g: rows 2i, 2i + 1 of its 16 x 256 slice; lane l
+    // takes slot l & 31 of row 2i + l / 32 (chunk (l & 31) ^ row).
+    // Registers, then LDS: the compiler orders the wave's own LDS write and
+    // reads.
     half8v xs[8];
-    {
+    auto load_x = [&](int g) {
       const int t0 = lane >> 5, s = lane & 31;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int t = 2 * i + t0;
-        xs[i] = *(const half8v*)(x + (size_t)min(t, M - 1) * ldx + 256 * blk + 8 * (s ^ t));
+        xs[i] = *(const half8v*)(x + (size_t)min(16 * g + t, M - 1) * ldx + 256 * blk + 8 * (s ^ t));
       }
-    }
+    };
+    load_x(0);
     Raw raw[kGvTiles];
 #pragma unroll
     for (int t = 0; t < kGvTiles; ++t) {
@@ -218,64 +224,82 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
       else
         raw[t].load(w, row_bytes, min(n0 + 16 * (t % P) + 64 * (t / P) + c, N - 1), blk, kq);
     }
+    half8v wf[kGvTiles][8];  // decoded fragments: run r -> 2r, 2r + 1
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *(half8v*)(sx + 1024 * i + 16 * lane) = xs[i];
-    half8v xa[8];
+    for (int g = 0; g < NG; ++g) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : TYPE == kQ6_K ? gv_q6k_run_k(kq, r) : gv_q40_run_k(kq, r);
-      xa[2 * r] = *(const half8v*)(sx + 512 * c + 16 * ((k >> 3) ^ c));
-      xa[2 * r + 1] = *(const half8v*)(sx + 512 * c + 16 * (((k >> 3) + 1) ^ c));
-    }
+      for (int i = 0; i < 8; ++i) *(half8v*)(sx + 1024 * i + 16 * lane) = xs[i];
+      if (g + 1 < NG) load_x(g + 1);
+      half8v xa[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int t = 0; t < kGvTiles; ++t) {
-        half8v f0, f1;
-        raw[t].run(kq, r, f0, f1);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r], f0, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r + 1], f1, acc[t], 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        const int k = TYPE == kQ4_K ? gv_q4k_run_k(kq, r) : TYPE == kQ6_K ? gv_q6k_run_k(kq, r) : gv_q40_run_k(kq, r);
+        xa[2 * r] = *(const half8v*)(sx + 512 * c + 16 * ((k >> 3) ^ c));
+        xa[2 * r + 1] = *(const half8v*)(sx + 512 * c + 16 * (((k >> 3) + 1) ^ c));
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < kGvTiles; ++t) {
+          if (g == 0) raw[t].run(kq, r, wf[t][2 * r], wf[t][2 * r + 1]);
+          acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r], wf[t][2 * r], acc[g][t], 0, 0, 0);
+          acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r + 1], wf[t][2 * r + 1], acc[g][t], 0, 0, 0);
+        }
+    }
   }
-  // The wave's sums replace its X slice (its fragment reads came first).
-  float4v* red = (float4v*)smem;  // [wave][tile][lane] at wave * kGvXSlice
+  // The 8 waves' sums are added in LDS in rounds of GR token groups (8 tile
+  // sums of 1 KB per wave, in the wave's X region: its fragment reads came
+  // first), each (tile, group) by one wave.
+  constexpr int GR = kGvWaves / kGvTiles, ROUNDS = (NG + GR - 1) / GR;
+  float4v* red = (float4v*)smem;  // round's sums: [wave][group - GR r][tile][lane] at wave * kGvXSlice
+  // D layout: lane l, register i -> token 16 g + 4 (l / 16) + i, row l % 16 of the tile.
+  auto tile_sum = [&](int pair) {
+    float4v s = red[pair * 64 + lane];
 #pragma unroll
-  for (int t = 0; t < kGvTiles; ++t) red[(wave * kGvXSlice / 16) + t * 64 + lane] = acc[t];
-  __syncthreads();
-
-  // D layout: lane l, register i -> token 4 (l / 16) + i, row l % 16 of the tile.
-  auto tile_sum = [&](int t) {
-    float4v s = red[t * 64 + lane];
-#pragma unroll
-    for (int v = 1; v < kGvWaves; ++v) s += red[v * (kGvXSlice / 16) + t * 64 + lane];
+    for (int v = 1; v < kGvWaves; ++v) s += red[v * (kGvXSlice / 16) + pair * 64 + lane];
     return s;
   };
-  if constexpr (MODE == kGvSwiGLU) {
-    if (wave >= P) return;
-    const float4v g = tile_sum(wave), u = tile_sum(wave + P);
-    const int f = 64 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G) + 16 * wave + c;
-    if (n0 + 16 * wave + c + 64 >= N) return;
-    uint16_t* y = (uint16_t*)out;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 4 * kq + i;
-      if (m >= M) continue;
-      const float gv = (float)(half_t)g[i], uv = (float)(half_t)u[i];
-      y[(size_t)m * ldo + f] = f2h(gv / (1.0f + expf(-gv)) * uv);
-    }
-  } else {
-    if (wave >= kGvTiles) return;
-    const float4v s = tile_sum(wave);
-    const int row = n0 + 16 * (wave % P) + 64 * (wave / P) + c;
-    if (row >= N) return;
+  for (int r = 0; r < ROUNDS; ++r) {
+    if (r > 0) __syncthreads();  // the previous round's sums have been read
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 4 * kq + i;
-      if (m >= M) continue;
-      if constexpr (MODE == kGvStore)
-        ((uint16_t*)out)[(size_t)m * ldo + row] = f2h(s[i]);
-      else
-        ((float*)out)[((size_t)blockIdx.y * M + m) * N + row] = s[i];
+    for (int gg = 0; gg < GR; ++gg)
+      if (GR * r + gg < NG)
+#pragma unroll
+        for (int t = 0; t < kGvTiles; ++t)
+          red[(wave * kGvXSlice / 16) + (gg * kGvTiles + t) * 64 + lane] = acc[min(GR * r + gg, NG - 1)][t];
+    __syncthreads();
+    if constexpr (MODE == kGvSwiGLU) {
+      // wave -> gate tile wave % P (and its up tile) of group GR r + wave / P
+      const int tp = wave % P, gg = wave / P, g = GR * r + gg;
+      const int f = 64 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G) + 16 * tp + c;
+      if (gg < GR && g < NG && n0 + 16 * tp + c + 64 < N) {
+        const float4v gs = tile_sum(gg * kGvTiles + tp), us = tile_sum(gg * kGvTiles + tp + P);
+        uint16_t* y = (uint16_t*)out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * g + 4 * kq + i;
+          if (m >= M) continue;
+          const float gv = (float)(half_t)gs[i], uv = (float)(half_t)us[i];
+          y[(size_t)m * ldo + f] = f2h(gv / (1.0f + expf(-gv)) * uv);
+        }
+      }
+    } else {
+      // wave -> tile wave % T of group GR r + wave / T
+      const int t = wave % kGvTiles, g = GR * r + wave / kGvTiles;
+      const int row = n0 + 16 * (t % P) + 64 * (t / P) + c;
+      if (g < NG && row < N) {
+        const float4v s = tile_sum(wave);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * g + 4 * kq + i;
+          if (m >= M) continue;
+          if constexpr (MODE == kGvStore)
+            ((uint16_t*)out)[(size_t)m * ldo + row] = f2h(s[i]);
+          else
+            ((float*)out)[((size_t)blockIdx.y * M + m) * N + row] = s[i];
+        }
+      }
     }
   }
 }
@@ -339,6 +363,28 @@ size_t gemv_partials_floats(const QWeight& w, int m) {
   return s > 1 ? (size_t)s * m * w.n : 0;
 }
 
+// One launch over NG >= ceil(m / 16) token groups (1, 2, 3, 4, 6 or 8;
+// groups past m are clamped loads whose sums are not stored).
+template <int TYPE, int MODE, int T, bool TILED>
+static void launch_gemv_groups(dim3 grid, const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
+                               hipStream_t stream) {
+  const int ng = (m + 15) / 16;
+  if (ng == 1)
+    gemv_kernel<TYPE, MODE, T, TILED, 1><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  else if (ng == 2)
+    gemv_kernel<TYPE, MODE, T, TILED, 2><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  else if constexpr (T <= 2) {
+    if (ng == 3)
+      gemv_kernel<TYPE, MODE, T, TILED, 3><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    else if (ng == 4)
+      gemv_kernel<TYPE, MODE, T, TILED, 4><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    else if (ng <= 6)
+      gemv_kernel<TYPE, MODE, T, TILED, 6><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    else
+      gemv_kernel<TYPE, MODE, T, TILED, 8><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  }
+}
+
 template <int TYPE, int MODE>
 static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
                                hipStream_t stream) {
@@ -348,25 +394,26 @@ static void launch_gemv_kernel(const uint16_t* x, int ldx, const QWeight& w, int
     // (or for SwiGLU), else 1 (measured on Q4_K: 16384 x 2048 7.7 us on 2
     // tiles, 7.9 on 4; 2048 x 2048 3.7 us on 1 against 4.5 untiled).
     if (MODE == kGvSwiGLU || 4 * groups * splits >= 256) {
-      gemv_kernel<TYPE, MODE, 2, true><<<dim3(4 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+      launch_gemv_groups<TYPE, MODE, 2, true>(dim3(4 * groups, splits), x, ldx, w, m, out, ldo, stream);
     } else {
       if constexpr (MODE != kGvSwiGLU)
-        gemv_kernel<TYPE, MODE, 1, true><<<dim3(8 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+        launch_gemv_groups<TYPE, MODE, 1, true>(dim3(8 * groups, splits), x, ldx, w, m, out, ldo, stream);
     }
     return;
   }
   // 4 tiles per wave (X fragments reused 4 times) once that alone gives
-  // every CU a workgroup; else 2 when that does (or for SwiGLU, whose gate
-  // and up tiles pair up); else 1, which spreads a small matrix over the
-  // most CUs (2048 x 2048: 128 workgroups, 1.2x faster than 64 of 2 tiles).
-  // A row's arithmetic is the same in every configuration.
-  if (2 * groups * splits >= 256) {
-    gemv_kernel<TYPE, MODE, 4><<<dim3(2 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+  // every CU a workgroup and m <= 32 (more token groups of 4 tiles
+  // outgrow the registers); else 2 when that does (or for
+  // SwiGLU, whose gate and up tiles pair up); else 1, which spreads a small
+  // matrix over the most CUs (2048 x 2048: 128 workgroups, 1.2x faster than
+  // 64 of 2 tiles). A row's arithmetic is the same in every configuration.
+  if (2 * groups * splits >= 256 && m <= 32) {
+    launch_gemv_groups<TYPE, MODE, 4, false>(dim3(2 * groups, splits), x, ldx, w, m, out, ldo, stream);
   } else if (MODE == kGvSwiGLU || 4 * groups * splits >= 256) {
-    gemv_kernel<TYPE, MODE, 2><<<dim3(4 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    launch_gemv_groups<TYPE, MODE, 2, false>(dim3(4 * groups, splits), x, ldx, w, m, out, ldo, stream);
   } else {
     if constexpr (MODE != kGvSwiGLU)
-      gemv_kernel<TYPE, MODE, 1><<<dim3(8 * groups, splits), 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+      launch_gemv_groups<TYPE, MODE, 1, false>(dim3(8 * groups, splits), x, ldx, w, m, out, ldo, stream);
   }
 }
 
@@ -463,7 +510,7 @@ static void launch_gemv_typed(const uint16_t* x, int ldx, const QWeight& w, int 
 hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, void* out, int ldo,
                           float* partials, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
-  if (m > 16 || (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0)) return hipErrorInvalidValue;
+  if (m > kGemvMaxM || (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0)) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
   const int splits = gemv_splits(w);
   if (epilogue == kEpiPartial) {

@@ -3,12 +3,12 @@
 
 Bar: cosine >= 0.9999 per embedding against the oracle (fp64 arithmetic, f16
 storage at the reference's points); |norm - 1| <= 0.01 (src/main.ts:218).
-Projections pick their kernels by the pass's token count in three regimes:
-at most 16 tokens (split-K GEMV), 17 to 64 (one 64-row tile, K split into
-chunks) and more (fused or two-pass tiles, K split by the weight's shape
-only). A request's embedding is bit-identical whether it runs alone or inside
-a ragged batch when both passes fall in the same regimes, and within cosine
-0.99999 otherwise (the reference accepts >= 0.999, src/main.ts:298).
+Projections pick their kernels by the pass's token count in two regimes: at
+most 128 tokens (the split-K GEMV) and more (fused or two-pass tiles), K split
+by the weight's shape only in both. A request's embedding is bit-identical
+whether it runs alone or inside a ragged batch when both passes fall in the
+same regimes, and within cosine 0.99999 otherwise (the reference accepts >=
+0.999, src/main.ts:298).
 """
 import numpy as np
 import pytest
@@ -25,9 +25,8 @@ def _cos(a, b):
 
 
 def _regime(m):
-    """Projection regime of a pass of m tokens: GEMV, split-K 64-row tile, or
-    the tiles whose K split depends on the weight only."""
-    return 0 if m <= 16 else 1 if m <= 64 else 2
+    """Projection regime of a pass of m tokens: the GEMV or the MFMA tiles."""
+    return 0 if m <= 128 else 1
 
 
 def _padded(seqs, seq_len, pad=11):
@@ -116,9 +115,10 @@ def test_request_past_16384_tokens_matches_oracle(torch_cuda):
 
 
 def test_small_batches_take_the_gemv_and_stay_batch_invariant(torch_cuda):
-    """Passes of at most 16 tokens run every projection on the split-K GEMV
-    (its split count depends only on the weight): results match the oracle
-    and are bit-identical whatever else shares the pass."""
+    """Passes of at most 128 tokens run every projection on the split-K GEMV
+    (its split count depends only on the weight, and a token's arithmetic
+    not on how many groups of 16 tokens share the pass): results match the
+    oracle and are bit-identical whatever else shares the pass."""
     dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, layers=3, vocab=300,
                         merge_after_layer=1)
     tensors = synth.model_tensors(dims, seed=91, embedding_type=14)
@@ -127,38 +127,45 @@ def test_small_batches_take_the_gemv_and_stay_batch_invariant(torch_cuda):
     seqs = [[1, 17, 250, 3, 99], [1, 2], [1], [1] + list(synth.randint(92, 7, 2, 300))]   # 16 tokens in all
     ids, lens = _padded(seqs, 8)
     got = model.createPlan(len(seqs), 8).run_sync(ids, lens)
+    # the same requests among 110 tokens (7 groups; 74 after the merge)
+    more = seqs + [[1] + list(synth.randint(93 + i, n - 1, 2, 300)) for i, n in enumerate((40, 54))]
+    ids2, lens2 = _padded(more[::-1], 54)
+    got2 = model.createPlan(len(more), 54).run_sync(ids2, lens2)
     for i, s in enumerate(seqs):
         assert _cos(got[i], oracle.forward_request(om, np.array(s))) >= 0.9999, f"request {i}"
         single = model.createPlan(1, len(s)).run_sync(np.array(s, dtype=np.uint32), [len(s)])[0]
         assert np.array_equal(single.view(np.uint32), got[i].view(np.uint32)), f"request {i} differs alone"
+        assert np.array_equal(single.view(np.uint32), got2[len(more) - 1 - i].view(np.uint32)), \
+            f"request {i} differs among 110 tokens"
+    for i in (4, 5):
+        assert _cos(got2[len(more) - 1 - i], oracle.forward_request(om, np.array(more[i]))) >= 0.9999
 
 
 def test_batch_invariance_across_regimes(torch_cuda):
-    """A request alone and inside a batch of more than 64 tokens: where its
+    """A request alone and inside a batch of more than 128 tokens: where its
     passes alone (before and after the merge) take the same regimes as the
-    batch's, the bits agree; where they take the 17-64 token split-K tiles,
-    cosine >= 0.99999; all match the oracle; two batches in the same regimes
-    give a shared request the same bits."""
-    # K of 1024 and 2048: the split-K regime cuts every projection in 2 or 4
+    batch's, the bits agree; where they take the GEMV, cosine >= 0.99999; all
+    match the oracle; two batches in the same regimes give a shared request
+    the same bits."""
     dims = rt.make_dims(hidden=1024, q_heads=8, kv_heads=2, head_dim=128, intermediate=2048, layers=2, vocab=400,
                         merge_after_layer=1)
     tensors = synth.model_tensors(dims, seed=93, embedding_type=1)
     model = rt.NemotronHipModel(tensors, dims=dims)
     om = synth.oracle_model(dims, tensors)
-    lengths = [120, 90, 200, 60, 30]   # alone: big/big, big/split, big/big, split/split, split/small
+    lengths = [260, 90, 220, 60, 30]   # alone: tiles/tiles, GEMV/GEMV, tiles/tiles, GEMV/GEMV, GEMV/GEMV
     seqs = [[1] + list(synth.randint(940 + i, n - 1, 2, 400)) for i, n in enumerate(lengths)]
-    ids, lens = _padded(seqs, 200)
-    got = model.createPlan(len(seqs), 200).run_sync(ids, lens)          # 500 tokens, 322 after the merge
-    ids2, lens2 = _padded(seqs[::-1], 200)
-    got2 = model.createPlan(len(seqs), 200).run_sync(ids2, lens2)
+    ids, lens = _padded(seqs, 260)
+    got = model.createPlan(len(seqs), 260).run_sync(ids, lens)          # 660 tokens, 425 after the merge
+    ids2, lens2 = _padded(seqs[::-1], 260)
+    got2 = model.createPlan(len(seqs), 260).run_sync(ids2, lens2)
     merged = lambda n: -(-n * 16 // 25)   # ceil(0.64 n)
-    assert (_regime(sum(lengths)), _regime(sum(map(merged, lengths)))) == (2, 2)
+    assert (_regime(sum(lengths)), _regime(sum(map(merged, lengths)))) == (1, 1)
     identical = 0
     for i, s in enumerate(seqs):
         assert np.array_equal(got[i].view(np.uint32), got2[len(seqs) - 1 - i].view(np.uint32)), f"request {i}"
         single = model.createPlan(1, len(s)).run_sync(np.array(s, dtype=np.uint32), [len(s)])[0]
         ref = oracle.forward_request(om, np.array(s))
-        if (_regime(len(s)), _regime(merged(len(s)))) == (2, 2):
+        if (_regime(len(s)), _regime(merged(len(s)))) == (1, 1):
             assert np.array_equal(single.view(np.uint32), got[i].view(np.uint32)), f"request {i} differs alone"
             identical += 1
         else:

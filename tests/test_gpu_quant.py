@@ -120,6 +120,44 @@ def test_matmul_vs_oracle(torch_cuda, type_, m, n, k, algo):
 
 
 @pytest.mark.parametrize("type_,m,n,k", [
+    (12, 17, 3072, 2048),    # two token groups, the last of one token
+    (12, 50, 2048, 2048),    # four groups on 2048 x 2048 (tiled copies, one tile per wave)
+    (14, 64, 2048, 8192),    # Q6_K, K split in four
+    (12, 33, 16384, 2048),   # three groups, two tiles per wave
+    (12, 40, 200, 512),      # rows not a multiple of 16 (untiled), two of eight waves with blocks
+    (12, 65, 3072, 2048),    # six groups (the last five clamped), sums added in two rounds
+    (12, 100, 16384, 2048),  # seven of eight groups, two tiles per wave
+    (14, 128, 2048, 8192),   # eight full groups, Q6_K split in four
+])
+def test_gemv_token_groups_vs_oracle(torch_cuda, type_, m, n, k):
+    """The GEMV on 17 to 128 tokens (each decoded weight fragment applied to
+    up to eight groups of 16 tokens): within the projection bar of the
+    oracle, and every token's row bit-identical to the same token run in a
+    pass of one group (its arithmetic does not depend on the pass size)."""
+    torch = torch_cuda
+    seed = 1301 + m + n + k
+    raw = (synth.random_q4k if type_ == 12 else synth.random_q6k)(seed, n * k // 256)
+    x16 = synth.normal(seed + 7, m * k).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(type_, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+
+    def gemv(rows, x_ptr):
+        dy = torch.zeros((rows, n), dtype=torch.int16, device="cuda")
+        w.matmul(x_ptr, rows, dy.data_ptr(), _lib.MATMUL_GEMV)
+        torch.cuda.synchronize()
+        return dy.cpu().numpy()
+
+    y = gemv(m, dx.data_ptr())
+    _check_matmul(y.view(np.float16), x16, oracle.dequantize(type_, raw).reshape(n, k))
+    for r0 in range(0, m, 16):
+        rows = min(16, m - r0)
+        part = gemv(rows, dx[r0:].data_ptr())
+        assert np.array_equal(part, y[r0:r0 + rows]), f"tokens {r0}..{r0 + rows} differ from the {m}-token pass"
+    with pytest.raises(rt.NemoError, match="GEMV takes m <= 128"):
+        w.matmul(dx.data_ptr(), 129, dx.data_ptr(), _lib.MATMUL_GEMV)
+
+
+@pytest.mark.parametrize("type_,m,n,k", [
     (12, 2400, 16384, 2048),   # the gate/up shape of 16 x 150 tokens: 256 x 256 LDS-copy tiles
     (14, 4096, 8192, 2048),
 ])
@@ -275,18 +313,18 @@ def test_q40_weights_dequantize_bit_exact(torch_cuda, n, k):
         assert _bits_equal(out.cpu().numpy(), expect), f"type {type_}"
 
 
-@pytest.mark.parametrize("m,n,k", [(15, 2048, 2048), (16, 12288, 2048), (150, 5120, 2048), (2400, 2048, 6144),
-                                   (333, 200, 768)])
+@pytest.mark.parametrize("m,n,k", [(15, 2048, 2048), (16, 12288, 2048), (50, 5120, 2048), (120, 2048, 2048), (150, 5120, 2048),
+                                   (2400, 2048, 6144), (333, 200, 768)])
 def test_q40_matmul_all_paths(torch_cuda, m, n, k):
     """The compact Q4_0 matrices of the reference's pack through the GEMV (m <=
-    16), the fused GEMM and the two-pass GEMM: within the projection bar of
+    128), the fused GEMM and the two-pass GEMM: within the projection bar of
     the oracle, and GEMM and two-pass bit-identical."""
     torch = torch_cuda
     raw, compact = _q40_pair(7000 + m + n, n, k)
     w = rt.QuantWeight(_lib.TYPE_Q4_0_TILE32, n, k, compact)
     x16 = synth.normal(7001 + m, m * k).astype(np.float16).reshape(m, k)
     dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
-    algos = [_lib.MATMUL_GEMM, _lib.MATMUL_TWO_PASS] + ([_lib.MATMUL_GEMV] if m <= 16 else [])
+    algos = [_lib.MATMUL_GEMM, _lib.MATMUL_TWO_PASS] + ([_lib.MATMUL_GEMV] if m <= 128 else [])
     outs = {}
     for algo in algos:
         dy = torch.zeros((m, n), dtype=torch.int16, device="cuda")
