@@ -710,8 +710,11 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
       mats.push_back(&w.o);
       mats.push_back(&w.down);
       for (const QWeight* q : mats) {
-        const int s = gemm_splits(*q);
-        if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * tf * q->n);
+        // the largest pass, and the largest below kLargeM (more splits)
+        for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)}) {
+          const int s = gemm_splits(*q, (int)m);
+          if (s > 1) partial_floats = std::max(partial_floats, (size_t)s * m * q->n);
+        }
       }
     }
     // Passes of at most kGemvMaxM tokens take the GEMV, whose split counts differ.
@@ -729,8 +732,9 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
       std::vector<const QWeight*> mats = qkv_matrices(w);
       mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
       for (const QWeight* q : mats)
-        if (gemm_two_pass(*q, (int)tf, gemm_splits(*q)))
-          wexp_halves = std::max(wexp_halves, (size_t)q->n * q->k);
+        for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)})
+          if (gemm_two_pass(*q, (int)m, gemm_splits(*q, (int)m)))
+            wexp_halves = std::max(wexp_halves, (size_t)q->n * q->k);
     }
     if (wexp_halves) p->wexp = dev_alloc(wexp_halves * 2, "f16 weight expansion");
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
@@ -870,7 +874,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     const bool small = M <= kGemvMaxM;
     // One matrix, or separate q / k / v parts each into its column range.
     auto qkv_proj = [&](const QWeight& wq, int col) {
-      const int sp = gemm_splits(wq);
+      const int sp = gemm_splits(wq, M);
       if (small) {
         hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
       } else if (sp == 1) {
@@ -898,7 +902,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
     auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
-      const int splits = small ? gemv_splits(wt) : gemm_splits(wt);
+      const int splits = small ? gemv_splits(wt) : gemm_splits(wt, M);
       mark(stage, true);
       if (small)
         hip_check(launch_gemv_ex(in, ldin, wt, M, splits == 1 ? kEpiStore : kEpiPartial,

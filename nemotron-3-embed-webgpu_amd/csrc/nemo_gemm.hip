@@ -595,14 +595,19 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
   gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo);
 }
 
-int gemm_splits(const QWeight& w) {
+int gemm_splits(const QWeight& w, int m) {
   // Narrow projections (N = hidden) give too few column tiles to fill 256
-  // CUs: split K into chunks of at least 1024 columns, at most 4 ways.
+  // CUs: split K into chunks of at least 1024 columns, at most 4 ways, or 2
+  // from kLargeM tokens on, where the f16 tiles fill the CUs with half the
+  // fp32 partials (Q6_K 2048 x 8192 at 2400 tokens: 101.8 us with its
+  // expansion on 2 splits against 117.1 on 4, and the RMSNorm that sums the
+  // partials 11.7 us against 17.0).
   const int ntiles = (w.n + 127) / 128;
   const int kblocks = w.k / 256;
   if (ntiles >= 24) return 1;
+  const int cap = m >= kLargeM ? 2 : 4;
   int s = 1;
-  while (s < 4 && kblocks % (2 * s) == 0 && w.k / (2 * s) >= 1024) s *= 2;
+  while (s < cap && kblocks % (2 * s) == 0 && w.k / (2 * s) >= 1024) s *= 2;
   return s;
 }
 
@@ -705,6 +710,23 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     if (main > 0 && main < m) {
       const int wg_main = (main / 256) * (w.n / 256), wg_rest = ((m - main + 127) / 128) * (w.n / 256);
       if (1000 * ((wg_main + 255) / 256) + 650 * ((wg_rest + 255) / 256) < cost) best = kF16T256Tail;
+    }
+    return best;
+  }
+  if (splits > 1 && m >= kLargeM && w.n % 256 == 0) {
+    // K split over too few column tiles for a round of 256-row tiles: the
+    // tiling with the fewest rounds of 256 workgroups, a round charged its
+    // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650).
+    // Measured (expansion included): Q6_K 2048 x 8192 in 2 splits at 2400
+    // tokens 101.8 us on 192 x 256 (256 x 256 105.8, 128 x 256 136.3), at 1536
+    // tokens 74.0 on 128 x 256 (192 x 256 99.0); Q4_K 2048 x 2048 in 2
+    // splits at 1536 tokens 29.8 on 128 x 256 against 30.3 fused.
+    const int tiles[3] = {kF16T256x256, kF16T192x256, kF16T128x256}, charge[3] = {1000, 904, 650};
+    int best = kF16None, cost = 0;
+    for (int i = 0; i < 3; ++i) {
+      const int wg = ((m + f16_bm(tiles[i]) - 1) / f16_bm(tiles[i])) * (w.n / 256) * splits;
+      const int c = charge[i] * ((wg + 255) / 256);
+      if (best == kF16None || c < cost) best = tiles[i], cost = c;
     }
     return best;
   }

@@ -53,9 +53,11 @@ hipError_t launch_gemm(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
 hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, uint16_t* y, int ldy,
                                 uint16_t* wexp, hipStream_t stream);
 
-// The K-split count the encoder uses for `w`: a function of the weight's
-// shape only.
-int gemm_splits(const QWeight& w);
+// The K-split count the encoder uses for `w` in a pass of m > kGemvMaxM
+// tokens: a function of the weight's shape and of whether m reaches
+// kLargeM (narrow projections split at most 2 ways from there on).
+constexpr int kLargeM = 1024;
+int gemm_splits(const QWeight& w, int m);
 
 // Whether launch_gemm_ex, given scratch, expands `w` to f16 before an f16 x
 // f16 MFMA GEMM (large batches) rather than decoding inside the GEMM.
