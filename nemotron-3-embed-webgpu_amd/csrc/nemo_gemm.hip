@@ -599,9 +599,10 @@ int gemm_splits(const QWeight& w, int m) {
   // Narrow projections (N = hidden) give too few column tiles to fill 256
   // CUs: split K into chunks of at least 1024 columns, at most 4 ways, or 2
   // from kLargeM tokens on, where the f16 tiles fill the CUs with half the
-  // fp32 partials (Q6_K 2048 x 8192 at 2400 tokens: 101.8 us with its
-  // expansion on 2 splits against 117.1 on 4, and the RMSNorm that sums the
-  // partials 11.7 us against 17.0).
+  // fp32 partials (Q6_K 2048 x 8192 at 2400 tokens: 107 us with its
+  // expansion on 2 splits against 122 on 4, and the RMSNorm that sums the
+  // partials 11.6 us against 17.0; at 1536 tokens 2 splits lose: 78.5 us
+  // against 71.0).
   const int ntiles = (w.n + 127) / 128;
   const int kblocks = w.k / 256;
   if (ntiles >= 24) return 1;
@@ -713,14 +714,14 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     }
     return best;
   }
-  if (splits > 1 && m >= kLargeM && w.n % 256 == 0) {
-    // K split over too few column tiles for a round of 256-row tiles: the
-    // tiling with the fewest rounds of 256 workgroups, a round charged its
-    // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650).
-    // Measured (expansion included): Q6_K 2048 x 8192 in 2 splits at 2400
-    // tokens 101.8 us on 192 x 256 (256 x 256 105.8, 128 x 256 136.3), at 1536
-    // tokens 74.0 on 128 x 256 (192 x 256 99.0); Q4_K 2048 x 2048 in 2
-    // splits at 1536 tokens 29.8 on 128 x 256 against 30.3 fused.
+  if (splits > 1 && m >= kLargeM && w.k / splits >= 2048 && w.n % 256 == 0) {
+    // K split in long chunks over too few column tiles for a round of
+    // 256-row tiles: the tiling with the fewest rounds of 256 workgroups, a
+    // round charged its tiles' relative time (256 rows 1000, 192 rows 904,
+    // 128 rows 650). Measured (expansion included): Q6_K 2048 x 8192 in 2
+    // splits at 2400 tokens 101.8 us on 192 x 256 (256 x 256 105.8, 128 x 256
+    // 136.3) against 140.8 fused. Chunks of 1024 (Q4_K 2048 x 2048 in 2
+    // splits) gain nothing over the fused tiles.
     const int tiles[3] = {kF16T256x256, kF16T192x256, kF16T128x256}, charge[3] = {1000, 904, 650};
     int best = kF16None, cost = 0;
     for (int i = 0; i < 3; ++i) {

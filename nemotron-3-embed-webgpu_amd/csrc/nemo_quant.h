@@ -56,7 +56,7 @@ hipError_t launch_gemm_two_pass(const uint16_t* x, int ldx, const QWeight& w, in
 // The K-split count the encoder uses for `w` in a pass of m > kGemvMaxM
 // tokens: a function of the weight's shape and of whether m reaches
 // kLargeM (narrow projections split at most 2 ways from there on).
-constexpr int kLargeM = 1024;
+constexpr int kLargeM = 2048;
 int gemm_splits(const QWeight& w, int m);
 
 // Whether launch_gemm_ex, given scratch, expands `w` to f16 before an f16 x

@@ -4,8 +4,8 @@
 Bar: cosine >= 0.9999 per embedding against the oracle (fp64 arithmetic, f16
 storage at the reference's points); |norm - 1| <= 0.01 (src/main.ts:218).
 Projections pick their kernels by the pass's token count in three regimes:
-at most 128 tokens (the split-K GEMV), 129 to 1023 and 1024 or more (fused or
-two-pass tiles; narrow projections split K at most 2 ways from 1024 tokens),
+at most 128 tokens (the split-K GEMV), 129 to 2047 and 2048 or more (fused or
+two-pass tiles; narrow projections split K at most 2 ways from 2048 tokens),
 K split by the weight's shape within each. A request's embedding is
 bit-identical whether it runs alone or inside a ragged batch when both passes
 fall in the same regimes, and within cosine 0.99999 otherwise (the reference
@@ -27,8 +27,8 @@ def _cos(a, b):
 
 def _regime(m):
     """Projection regime of a pass of m tokens: the GEMV, or the MFMA tiles
-    below or from 1024 tokens."""
-    return 0 if m <= 128 else 1 if m < 1024 else 2
+    below or from 2048 tokens."""
+    return 0 if m <= 128 else 1 if m < 2048 else 2
 
 
 def _padded(seqs, seq_len, pad=11):
