@@ -316,3 +316,26 @@ def test_reference_dims_full_batch_matches_oracle(torch_cuda):
         ref = oracle.forward_request(om, ids[b * 150:(b + 1) * 150].astype(np.int64))
         c = _cos(got[b], ref)
         assert c >= 0.9999, f"request {b}: cosine {c:.6f}"
+
+
+def test_passes_from_2048_tokens_split_down_two_ways(torch_cuda):
+    """A down projection of K 4096 splits K 4 ways below 2048 tokens and 2
+    ways from there: a request shared by two batches of 2048 tokens or more
+    keeps its bits, and agrees with itself run alone (below 2048) to cosine
+    0.99999 and with the oracle to 0.9999."""
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=4096, layers=2, vocab=300,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=95, embedding_type=14)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    shared = [1] + list(synth.randint(960, 1199, 2, 300))
+    outs = []
+    for other in (1000, 900):   # 2200 and 2100 tokens, 1408 and 1344 after the merge
+        seqs = [shared, [1] + list(synth.randint(961 + other, other - 1, 2, 300))]
+        assert _regime(sum(map(len, seqs))) == 2
+        ids, lens = _padded(seqs, 1200)
+        outs.append(model.createPlan(2, 1200).run_sync(ids, lens)[0])
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    alone = model.createPlan(1, 1200).run_sync(np.array(shared, dtype=np.uint32), [1200])[0]
+    assert _cos(alone, outs[0]) >= 0.99999, f"cosine {_cos(alone, outs[0])}"
+    assert _cos(outs[0], oracle.forward_request(om, np.array(shared))) >= 0.9999
