@@ -732,10 +732,13 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     return best;
   }
   if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) {
-    // 128 x 128 tiles (2 waves) when 256-row tiles leave CUs without a
-    // workgroup and 128-row tiles do not (the QKV projection at 1536
-    // tokens: 288 workgroups, 32.6 us against 35.3 on 144 of 256 x 128).
-    if (mt * (w.n / 128) < 256 && ((m + 127) / 128) * (w.n / 128) >= 256) return kF16T128x128;
+    // 128-row tiles when 256-row tiles leave CUs without a workgroup and
+    // 128 x 128 tiles would not: 128 x 256 on 8 waves where the columns
+    // allow, else 128 x 128 on 4 waves (the QKV projection's f16 GEMM at
+    // 1536 tokens: 34.9 us on 144 workgroups of 128 x 256, 36.4 on 288 of
+    // 128 x 128; at 2400 tokens 39.4 and 40.6).
+    if (mt * (w.n / 128) < 256 && ((m + 127) / 128) * (w.n / 128) >= 256)
+      return w.n % 256 == 0 ? kF16T128x256 : kF16T128x128;
     return kF16T256x128;
   }
   return kF16None;
@@ -787,15 +790,15 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
       const int main = tail_main_rows(m, w.n), rest = m - main;
       launch_f16<256, 4, 2>(epilogue, dim3(w.n / 256, main / 256, 1), x, ldx, wexp, w, main, kchunk, out, ldo, stream);
       const size_t skip = (size_t)main * ldo * (epilogue == kEpiPartial ? 4 : 2);  // bytes of the rows done
-      launch_f16<256, 2, 2>(epilogue, dim3(w.n / 256, (rest + 127) / 128, 1), x + (size_t)main * ldx, ldx, wexp, w,
+      launch_f16<256, 4, 1>(epilogue, dim3(w.n / 256, (rest + 127) / 128, 1), x + (size_t)main * ldx, ldx, wexp, w,
                             rest, kchunk, (uint8_t*)out + skip, ldo, stream);
       break;
     }
     case kF16T256x256: launch_f16<256, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T256x128: launch_f16<128, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T192x256: launch_f16<256, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T128x256: launch_f16<256, 2, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T128x128: launch_f16<128, 2, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T128x256: launch_f16<256, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T128x128: launch_f16<128, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

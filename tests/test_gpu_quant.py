@@ -187,7 +187,8 @@ def test_matmul_large_tiles_vs_oracle(torch_cuda, type_, m, n, k):
     (12, 1536, 16384, 2048),   # after the merge: 1024 rows of 256 x 256 tiles, 512 of 128 x 256
     (12, 5000, 16384, 2048),   # whole rounds of 256 x 256 tiles only
     (14, 2400, 2048, 8192),    # down: 192 x 256 tiles
-    (12, 1536, 3072, 2048),    # QKV after the merge: 128 x 128 tiles
+    (12, 1536, 3072, 2048),    # QKV after the merge: 128 x 256 tiles on 8 waves
+    (12, 1536, 3200, 2048),    # columns not a multiple of 256: 128 x 128 tiles on 4 waves
     (12, 333, 200, 768),       # ragged rows and columns: clamped tile edges
     (14, 70, 384, 512),
 ])
