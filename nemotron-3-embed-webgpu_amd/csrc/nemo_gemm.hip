@@ -714,14 +714,14 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     }
     return best;
   }
-  if (splits > 1 && m >= kLargeM && w.k / splits >= 2048 && w.n % 256 == 0) {
-    // K split in long chunks over too few column tiles for a round of
-    // 256-row tiles: the tiling with the fewest rounds of 256 workgroups, a
-    // round charged its tiles' relative time (256 rows 1000, 192 rows 904,
-    // 128 rows 650). Measured (expansion included): Q6_K 2048 x 8192 in 2
-    // splits at 2400 tokens 101.8 us on 192 x 256 (256 x 256 105.8, 128 x 256
-    // 136.3) against 140.8 fused. Chunks of 1024 (Q4_K 2048 x 2048 in 2
-    // splits) gain nothing over the fused tiles.
+  if (splits > 1 && w.n % 256 == 0) {
+    // K split over too few column tiles for a round of 256-row tiles: the
+    // tiling with the fewest rounds of 256 workgroups, a round charged its
+    // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650).
+    // Measured (expansion included): Q6_K 2048 x 8192 in 2 splits at 2400
+    // tokens 101.8 us on 192 x 256 (256 x 256 105.8) against 140.8 fused;
+    // Q4_K 2048 x 2048 in 2 splits at 1536 tokens 27.7 us on 128 x 256
+    // against 30.2 fused, at 2400 tokens 38.4 on 192 x 256 against 39.7.
     const int tiles[3] = {kF16T256x256, kF16T192x256, kF16T128x256}, charge[3] = {1000, 904, 650};
     int best = kF16None, cost = 0;
     for (int i = 0; i < 3; ++i) {
