@@ -326,6 +326,9 @@ __global__ __launch_bounds__(256) void attention_prep_kernel(const uint16_t* __r
   }
 }
 
+// Fewest threads per block that the prepared path's staging supports.
+constexpr int attn_prep_min_threads(int hd) { return hd == 128 ? 128 : 64; }
+
 template <int HD, bool PREP>
 __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
                                                         const float* __restrict__ table, Ragged rows, int q_heads,
@@ -380,63 +383,16 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  for (int sb = 0; sb < n_keys; sb += sb_keys) {
-    const int staged = min(sb_keys, n_keys - sb);
-    __syncthreads();
-    if constexpr (PREP) {
-      const uint16_t* kp = ks + ((size_t)kvh * keys_cap + koff + sb) * HD;
-      const int kch = (staged + 31) / 32 * 32 * HD / 8;  // whole 32-key blocks (zero-padded in K_s)
-      for (int i = threadIdx.x; i < kch; i += blockDim.x)
-        *(half8v*)&sK[(i / (HD / 8)) * KP + (i % (HD / 8)) * 8] = *(const half8v*)(kp + 8 * i);
-      const int vch = (staged + 31) / 32 * 4;  // 8-key chunks of a V^T row
-      for (int i = threadIdx.x; i < HD * vch; i += blockDim.x) {
-        const int d = i / vch, k0 = (i % vch) * 8;
-        *(half8v*)&sVt[d * VP + k0] = *(const half8v*)(vts + ((size_t)kvh * HD + d) * keys_cap + koff + sb + k0);
-      }
-    } else {
-      // 16-byte chunks of the staged keys (rows past `staged` up to the
-      // next multiple of 32 are zero), in batches of 4 per thread with every
-      // load of a batch issued before the first is used.
-      const int chunks = (staged + 31) / 32 * 32 * HD / 8;
-      for (int i0 = threadIdx.x; i0 < chunks; i0 += 4 * blockDim.x) {
-        half8v kr[4], vr[4];
-        float4v ca[4], cb[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-          kr[u] = half8v{};
-          vr[u] = half8v{};
-          ca[u] = cb[u] = float4v{0.f, 0.f, 0.f, 0.f};
-          if (i < chunks && j < staged) {
-            const int kpos = (sb + j) * key_stride;
-            const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
-            kr[u] = *(const half8v*)(kbase + trow + c);
-            vr[u] = *(const half8v*)(vbase + trow + c);
-            const float* cs = table + (size_t)kpos * HD + c;
-            ca[u] = *(const float4v*)cs;
-            cb[u] = *(const float4v*)(cs + 4);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
-          if (i < chunks) {
-            *(half8v*)&sK[j * KP + c] = rope8(kr[u], ca[u], cb[u]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sVt[(c + e) * VP + j] = vr[u][e];
-          }
-        }
-      }
-    }
-    __syncthreads();
-  for (int kb = 0; kb < staged; kb += kAttnKeys) {
+  // One block of kAttnKeys staged keys from key kb of cK [keys][KP] and
+  // cV [HD][vp]; keys at or past `staged` are masked.
+  auto block = [&](const half_t* cK, const half_t* cV, int vp, int kb, int staged) {
     // S^T block: lane holds query l%32, key kb + 8(r/4) + 4hl + r%4.
     float16v s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      const half8v a = *(const half8v*)&sK[(kb + (lane & 31)) * KP + 16 * c + 8 * hl];
+      const half8v a = *(const half8v*)&cK[(kb + (lane & 31)) * KP + 16 * c + 8 * hl];
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
     }
     float bm = -INFINITY;
@@ -470,14 +426,105 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
       const half8v pb = to_half8(p + 8 * c2);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const half_t* vr = &sVt[(32 * db + (lane & 31)) * VP + kb + 16 * c2 + 4 * hl];
+        const half_t* vr = &cV[(32 * db + (lane & 31)) * vp + kb + 16 * c2 + 4 * hl];
         const half4v v0 = *(const half4v*)vr;
         const half4v v1 = *(const half4v*)(vr + 8);
         const half8v a = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[db], 0, 0, 0);
       }
     }
-  }
+  };
+  if constexpr (PREP) {
+    // Rounds of kAttnKeys keys from K_s / V^T_s (zero-padded to whole
+    // rounds), double-buffered in LDS: each thread's 16-byte chunks of
+    // round r + 2 are loaded into registers while round r is computed and
+    // stored after it, so one barrier per round remains and a round's loads
+    // have a whole round to land.
+    constexpr int RK = kAttnKeys, VPR = RK + 8;
+    constexpr int KCH = RK * HD / 8, VCH = HD * (RK / 8);  // chunks of a round's K rows and V^T rows
+    constexpr int U = KCH / attn_prep_min_threads(HD);      // slots per thread at the smallest block
+    static_assert(KCH == VCH && KCH % attn_prep_min_threads(HD) == 0, "K and V^T chunks share the slots");
+    constexpr int STAGE = RK * KP + HD * VPR;               // halves per LDS stage
+    const int rounds = (n_keys + RK - 1) / RK;
+    const uint16_t* kp = ks + ((size_t)kvh * keys_cap + koff) * HD;
+    const uint16_t* vp0 = vts + (size_t)kvh * HD * keys_cap + koff;
+    half8v kr[U], vr[U];
+    auto load = [&](int r) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = threadIdx.x + u * blockDim.x;
+        if (i < KCH) {
+          kr[u] = *(const half8v*)(kp + (size_t)r * RK * HD + 8 * i);
+          const int d = i / (RK / 8), k0 = (i % (RK / 8)) * 8;
+          vr[u] = *(const half8v*)(vp0 + (size_t)d * keys_cap + r * RK + k0);
+        }
+      }
+    };
+    auto store = [&](int stage) {
+      half_t* dK = sK + stage * STAGE;
+      half_t* dV = dK + RK * KP;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = threadIdx.x + u * blockDim.x;
+        if (i < KCH) {
+          *(half8v*)&dK[(i / (HD / 8)) * KP + (i % (HD / 8)) * 8] = kr[u];
+          *(half8v*)&dV[(i / (RK / 8)) * VPR + (i % (RK / 8)) * 8] = vr[u];
+        }
+      }
+    };
+    load(0);
+    store(0);
+    if (rounds > 1) load(1);
+    __syncthreads();
+    for (int r = 0; r < rounds; ++r) {
+      const half_t* cK = sK + (r & 1) * STAGE;
+      block(cK, cK + RK * KP, VPR, 0, min(RK, n_keys - r * RK));
+      if (r + 1 < rounds) {
+        store((r + 1) & 1);
+        if (r + 2 < rounds) load(r + 2);
+      }
+      __syncthreads();
+    }
+  } else {
+    for (int sb = 0; sb < n_keys; sb += sb_keys) {
+      const int staged = min(sb_keys, n_keys - sb);
+      __syncthreads();
+      // 16-byte chunks of the staged keys (rows past `staged` up to the
+      // next multiple of 32 are zero), in batches of 4 per thread with every
+      // load of a batch issued before the first is used.
+      const int chunks = (staged + 31) / 32 * 32 * HD / 8;
+      for (int i0 = threadIdx.x; i0 < chunks; i0 += 4 * blockDim.x) {
+        half8v kr[4], vr[4];
+        float4v ca[4], cb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
+          kr[u] = half8v{};
+          vr[u] = half8v{};
+          ca[u] = cb[u] = float4v{0.f, 0.f, 0.f, 0.f};
+          if (i < chunks && j < staged) {
+            const int kpos = (sb + j) * key_stride;
+            const size_t trow = (size_t)(row0 + kpos) * qkv_stride;
+            kr[u] = *(const half8v*)(kbase + trow + c);
+            vr[u] = *(const half8v*)(vbase + trow + c);
+            const float* cs = table + (size_t)kpos * HD + c;
+            ca[u] = *(const float4v*)cs;
+            cb[u] = *(const float4v*)(cs + 4);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * blockDim.x, j = i / (HD / 8), c = (i % (HD / 8)) * 8;
+          if (i < chunks) {
+            *(half8v*)&sK[j * KP + c] = rope8(kr[u], ca[u], cb[u]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sVt[(c + e) * VP + j] = vr[u][e];
+          }
+        }
+      }
+      __syncthreads();
+      for (int kb = 0; kb < staged; kb += kAttnKeys) block(sK, sVt, VP, kb, staged);
+    }
   }
   if (qi >= n) return;
   const float inv = 1.0f / lsum;
@@ -512,7 +559,10 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
   const int group = q_heads / kv_heads;
   if (group < 1 || group > 8 || q_heads % kv_heads) return hipErrorInvalidValue;
   if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
-  const bool prep = ks != nullptr;
+  // The prepared path's register slots cover a round with 64 threads per
+  // 16 dims of the head (one wave at head_dim 64, two at 128); smaller
+  // blocks stage from the projection instead.
+  const bool prep = ks != nullptr && 64 * group >= attn_prep_min_threads(head_dim);
   if (prep) {
     const int keys = attention_prep_keys(rows, stride_threshold, key_stride);
     if (!vts || keys > keys_cap) return hipErrorInvalidValue;
@@ -527,7 +577,8 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
   dim3 grid(tiles, kv_heads);
   // Keys staged per round: every key of the pass's longest request when
   // they fit in ~72 KB of LDS and short requests only (one round of loads
-  // and barriers instead of one per 32 keys); 32 for the prepared path.
+  // and barriers instead of one per 32 keys); 32 for the prepared path, in
+  // two LDS stages.
   int longest_keys = 0;
   for (int b = 0; b < rows.count; ++b) {
     const int n = rows.start[b + 1] - rows.start[b];
@@ -536,7 +587,7 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
   }
   const int cap = 16384 / head_dim;  // 256 keys at head_dim 64, 128 at 128
   const int sb = prep ? kAttnKeys : std::min(cap, (longest_keys + kAttnKeys - 1) / kAttnKeys * kAttnKeys);
-  const int lds = 2 * (sb * (head_dim + 8) + head_dim * (sb + 8));
+  const int lds = (prep ? 2 : 1) * 2 * (sb * (head_dim + 8) + head_dim * (sb + 8));  // prepared: two stages
 #define NEMO_ATTN(HD, P)                                                                                           \
   attention_kernel<HD, P><<<grid, 64 * group, lds, stream>>>(qkv, qkv_stride, rope_table, rows, q_heads, kv_heads, \
                                                              stride_threshold, key_stride, ks, vts, keys_cap, sb, out)
