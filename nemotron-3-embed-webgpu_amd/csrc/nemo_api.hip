@@ -689,7 +689,7 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     p->norm_red = dev_alloc(tr * H * 2, "merged normalized hidden state");
     p->qkv = dev_alloc(tf * QKV * 2, "query + key + value raw");
     p->attn = dev_alloc(tf * QW * 2, "attention");
-    if (sequence >= kAttnPrepRows) {
+    if (sequence > attn_round_keys(d.head_dim)) {
       p->attn_keys_cap = batch * ((sequence + 31) / 32 * 32);
       const size_t halves = (size_t)d.kv_heads * p->attn_keys_cap * d.head_dim;
       p->attn_ks = dev_alloc(halves * 2, "attention keys");
@@ -889,11 +889,11 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     mark(2, false);
     mark(3, true);
     p->last_rows = rows;
-    // Requests of kAttnPrepRows rows or more: keys rotated and values
-    // transposed once per layer instead of once per 32-query tile.
+    // Requests longer than one staging round of keys: keys rotated and
+    // values transposed once per layer instead of once per 32-query tile.
     int longest = 0;
     for (int b = 0; b < rows.count; ++b) longest = std::max(longest, rows.start[b + 1] - rows.start[b]);
-    const bool prep = p->attn_ks && longest >= kAttnPrepRows;
+    const bool prep = p->attn_ks && longest > attn_round_keys(d.head_dim);
     hip_check(launch_attention(qkv, QKV, rope, rows, d.q_heads, d.kv_heads, d.head_dim, d.kv_stride_threshold,
                                d.kv_stride, attn, s, prep ? (uint16_t*)p->attn_ks.get() : nullptr,
                                prep ? (uint16_t*)p->attn_vts.get() : nullptr, p->attn_keys_cap),

@@ -43,10 +43,13 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
 // Keys the prepared buffers hold for `rows` (each request's attended keys
 // rounded up to 32).
 int attention_prep_keys(const Ragged& rows, int stride_threshold, int key_stride);
-// The plan prepares keys when a pass holds a request of at least this many
-// rows (measured on one request at head_dim 128: 1500 rows 12 % faster, 3200
-// 38 %, 5000 19 %; 16 x 150 rows 40 % slower).
-constexpr int kAttnPrepRows = 512;
+// Keys that one staging round of the attention holds in ~72 KB of LDS (256
+// at head_dim 64, 128 at 128). The plan prepares keys when a pass holds a
+// request longer than that (whole requests at head_dim 128: 300 tokens 3 %
+// faster than staging from the projection, 500 5 %, 16 x 500 4 %, 150
+// equal; at head_dim 64, 16 x 150 tokens in one round is 0.8 % faster than
+// prepared).
+constexpr int attn_round_keys(int head_dim) { return 16384 / head_dim; }
 
 // out[t, :F] = f16(silu(g) * u), g = gu[t, :F], u = gu[t, F:2F].
 hipError_t launch_swiglu(const uint16_t* gu, int rows, int f, uint16_t* out, hipStream_t stream);

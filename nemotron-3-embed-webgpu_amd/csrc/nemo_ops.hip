@@ -585,7 +585,7 @@ hipError_t launch_attention(const uint16_t* qkv, int qkv_stride, const float* ro
     const int s = n > stride_threshold ? key_stride : 1;
     longest_keys = std::max(longest_keys, (n + s - 1) / s);
   }
-  const int cap = 16384 / head_dim;  // 256 keys at head_dim 64, 128 at 128
+  const int cap = attn_round_keys(head_dim);
   const int sb = prep ? kAttnKeys : std::min(cap, (longest_keys + kAttnKeys - 1) / kAttnKeys * kAttnKeys);
   const int lds = (prep ? 2 : 1) * 2 * (sb * (head_dim + 8) + head_dim * (sb + 8));  // prepared: two stages
 #define NEMO_ATTN(HD, P)                                                                                           \

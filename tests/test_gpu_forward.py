@@ -78,13 +78,15 @@ def test_forward_matches_oracle(torch_cuda, cfg):
             assert _cos(single, oracle.forward_request(om, np.array(s))) >= 0.9999
 
 
-@pytest.mark.parametrize("hd", [64, 128])
-def test_long_requests_prepared_keys_match_oracle(torch_cuda, hd):
-    """A pass holding a request of 512 rows or more rotates the attended keys
-    and transposes the values once (the attention's preparation pass) instead
-    of once per query tile: ragged long and short requests, stride-3 keys for
-    those longer than 400, both layers before the merge."""
-    Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
+@pytest.mark.parametrize("hd,Hq,Hkv", [(64, 4, 2), (128, 2, 1), (128, 2, 2)])
+def test_long_requests_prepared_keys_match_oracle(torch_cuda, hd, Hq, Hkv):
+    """A pass holding a request longer than one staging round of keys (256 at
+    head_dim 64, 128 at 128) rotates the attended keys and transposes the
+    values once (the attention's preparation pass) instead of once per query
+    tile: ragged long and short requests, stride-3 keys for
+    those longer than 400, both layers before the merge. One-wave blocks at
+    head_dim 128 (as many KV heads as query heads) stage from the projection
+    instead."""
     dims = rt.make_dims(hidden=256, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=512, layers=2, vocab=300,
                         merge_after_layer=2, kv_stride_threshold=400)
     tensors = synth.model_tensors(dims, seed=707 + hd, embedding_type=1)
