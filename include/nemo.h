@@ -164,9 +164,9 @@ nemo_status nemo_weight_create(nemo_ctx* ctx, int32_t ggml_type, int32_t n, int3
                                size_t n_bytes, nemo_weight** out);
 nemo_status nemo_weight_destroy(nemo_weight* weight);
 
-#define NEMO_MATMUL_AUTO 0     /* GEMV for m <= 128, two-pass where it pays, else the fused GEMM */
+#define NEMO_MATMUL_AUTO 0     /* GEMV for m <= 160, two-pass where it pays, else the fused GEMM */
 #define NEMO_MATMUL_GEMM 1     /* MFMA GEMM decoding W inside the kernel (tiles chosen by size) */
-#define NEMO_MATMUL_GEMV 2     /* split-K GEMV, m <= 128 */
+#define NEMO_MATMUL_GEMV 2     /* split-K GEMV, m <= 160 */
 #define NEMO_MATMUL_TWO_PASS 3 /* W expanded to f16 scratch (n * k halves, held by the weight),
                                   then an f16 MFMA GEMM; bit-identical to NEMO_MATMUL_GEMM */
 #define NEMO_MATMUL_GEMM_MID 4 /* the fused GEMM on 64-row tiles with deep prefetch (the plan's choice

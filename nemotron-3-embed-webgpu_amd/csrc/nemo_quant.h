@@ -100,9 +100,9 @@ hipError_t launch_reduce_swiglu(const float* partials, int splits, int m, int n,
 
 // Small-M path (m <= kGemvMaxM): MFMA GEMV, 64 rows x 2048 K per workgroup
 // with an in-workgroup reduction, every decoded weight fragment applied to up
-// to 8 groups of 16 tokens; K beyond 2048 splits into fp32 partials summed in
+// to 10 groups of 16 tokens; K beyond 2048 splits into fp32 partials summed in
 // split order through `partials` (float, at least gemv_partials_floats()).
-constexpr int kGemvMaxM = 128;
+constexpr int kGemvMaxM = 160;
 size_t gemv_partials_floats(const QWeight& w, int m);
 // The GEMV's K-split count: a function of the weight's shape only.
 int gemv_splits(const QWeight& w);

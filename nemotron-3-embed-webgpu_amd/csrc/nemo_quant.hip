@@ -1,5 +1,5 @@
 // Quantized-weight kernels for gfx950 besides the GEMM: the split-K
-// wavefront GEMV (m <= 128), GGML Q4_K / Q6_K / Q4_0 block decoding to
+// wavefront GEMV (m <= 160), GGML Q4_K / Q6_K / Q4_0 block decoding to
 // float32/f16 (bit-exact with src/gguf/quantization.ts:19-74), and the
 // fixed-order reduction of split-K partial sums.
 #include <type_traits>
@@ -11,7 +11,7 @@
 namespace nemo {
 
 // ---------------------------------------------------------------------------
-// GEMV for m <= 128 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
+// GEMV for m <= 160 on v_mfma_f32_16x16x32_f16. A workgroup of 8 waves owns
 // 16 T weight rows (T = 1, 2 or 4 tiles of 16) and 8 consecutive 256-value
 // blocks of K: wave w takes block 8 * blockIdx.y + w of all T tiles. A wave
 // issues all of its weight loads before their first use (one memory round
@@ -363,7 +363,7 @@ size_t gemv_partials_floats(const QWeight& w, int m) {
   return s > 1 ? (size_t)s * m * w.n : 0;
 }
 
-// One launch over NG >= ceil(m / 16) token groups (1, 2, 3, 4, 6 or 8;
+// One launch over NG >= ceil(m / 16) token groups (1, 2, 3, 4, 6, 8 or 10;
 // groups past m are clamped loads whose sums are not stored).
 template <int TYPE, int MODE, int T, bool TILED>
 static void launch_gemv_groups(dim3 grid, const uint16_t* x, int ldx, const QWeight& w, int m, void* out, int ldo,
@@ -380,8 +380,10 @@ static void launch_gemv_groups(dim3 grid, const uint16_t* x, int ldx, const QWei
       gemv_kernel<TYPE, MODE, T, TILED, 4><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
     else if (ng <= 6)
       gemv_kernel<TYPE, MODE, T, TILED, 6><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
-    else
+    else if (ng <= 8)
       gemv_kernel<TYPE, MODE, T, TILED, 8><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
+    else
+      gemv_kernel<TYPE, MODE, T, TILED, 10><<<grid, 64 * kGvWaves, 0, stream>>>(x, ldx, w, m, out, ldo);
   }
 }
 

@@ -128,10 +128,12 @@ def test_matmul_vs_oracle(torch_cuda, type_, m, n, k, algo):
     (12, 65, 3072, 2048),    # six groups (the last five clamped), sums added in two rounds
     (12, 100, 16384, 2048),  # seven of eight groups, two tiles per wave
     (14, 128, 2048, 8192),   # eight full groups, Q6_K split in four
+    (12, 150, 3072, 2048),   # ten groups (the last of six tokens), one tile per wave, sums in two rounds
+    (12, 160, 16384, 2048),  # ten full groups, two tiles per wave, sums in three rounds
 ])
 def test_gemv_token_groups_vs_oracle(torch_cuda, type_, m, n, k):
-    """The GEMV on 17 to 128 tokens (each decoded weight fragment applied to
-    up to eight groups of 16 tokens): within the projection bar of the
+    """The GEMV on 17 to 160 tokens (each decoded weight fragment applied to
+    up to ten groups of 16 tokens): within the projection bar of the
     oracle, and every token's row bit-identical to the same token run in a
     pass of one group (its arithmetic does not depend on the pass size)."""
     torch = torch_cuda
@@ -153,8 +155,8 @@ def test_gemv_token_groups_vs_oracle(torch_cuda, type_, m, n, k):
         rows = min(16, m - r0)
         part = gemv(rows, dx[r0:].data_ptr())
         assert np.array_equal(part, y[r0:r0 + rows]), f"tokens {r0}..{r0 + rows} differ from the {m}-token pass"
-    with pytest.raises(rt.NemoError, match="GEMV takes m <= 128"):
-        w.matmul(dx.data_ptr(), 129, dx.data_ptr(), _lib.MATMUL_GEMV)
+    with pytest.raises(rt.NemoError, match="GEMV takes m <= 160"):
+        w.matmul(dx.data_ptr(), 161, dx.data_ptr(), _lib.MATMUL_GEMV)
 
 
 @pytest.mark.parametrize("type_,m,n,k", [
@@ -318,14 +320,14 @@ def test_q40_weights_dequantize_bit_exact(torch_cuda, n, k):
                                    (2400, 2048, 6144), (333, 200, 768)])
 def test_q40_matmul_all_paths(torch_cuda, m, n, k):
     """The compact Q4_0 matrices of the reference's pack through the GEMV (m <=
-    128), the fused GEMM and the two-pass GEMM: within the projection bar of
+    160), the fused GEMM and the two-pass GEMM: within the projection bar of
     the oracle, and GEMM and two-pass bit-identical."""
     torch = torch_cuda
     raw, compact = _q40_pair(7000 + m + n, n, k)
     w = rt.QuantWeight(_lib.TYPE_Q4_0_TILE32, n, k, compact)
     x16 = synth.normal(7001 + m, m * k).astype(np.float16).reshape(m, k)
     dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
-    algos = [_lib.MATMUL_GEMM, _lib.MATMUL_TWO_PASS] + ([_lib.MATMUL_GEMV] if m <= 128 else [])
+    algos = [_lib.MATMUL_GEMM, _lib.MATMUL_TWO_PASS] + ([_lib.MATMUL_GEMV] if m <= 160 else [])
     outs = {}
     for algo in algos:
         dy = torch.zeros((m, n), dtype=torch.int16, device="cuda")
