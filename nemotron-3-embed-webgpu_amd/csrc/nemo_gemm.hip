@@ -665,8 +665,13 @@ static int gemm_variant(const QWeight& w, int m, int splits) {
 // CU: there a step's latency, not the machine's throughput, bounds the other
 // kernels (measured on the encoder's shapes, 17 <= m <= 1024).
 static bool use_mid(const QWeight& w, int m, int splits) {
+  // Up to 512 workgroups, 256 for Q6_K, whose fused decode costs more (its
+  // 2048 x 8192 matrix in 4 splits at 320 tokens: 41.0 us on 320 workgroups
+  // of 64-row tiles against 33.7 expanded onto 128 x 128 tiles; at 192
+  // tokens 26.6 against 33.1).
   const int steps = w.k / splits / kBK;
-  return steps % kMidDepth == 0 && ((m + kMidBM - 1) / kMidBM) * ((w.n + 127) / 128) * splits <= 512;
+  const int wg = ((m + kMidBM - 1) / kMidBM) * ((w.n + 127) / 128) * splits;
+  return steps % kMidDepth == 0 && wg <= (w.type == kQ6_K ? 256 : 512);
 }
 
 // f16 GEMM tile configurations of the two-pass path.
@@ -717,28 +722,33 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
   if (splits > 1 && w.n % 256 == 0) {
     // K split over too few column tiles for a round of 256-row tiles: the
     // tiling with the fewest rounds of 256 workgroups, a round charged its
-    // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650).
+    // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650,
+    // 128 x 128 380).
     // Measured (expansion included): Q6_K 2048 x 8192 in 2 splits at 2400
     // tokens 101.8 us on 192 x 256 (256 x 256 105.8) against 140.8 fused;
     // Q4_K 2048 x 2048 in 2 splits at 1536 tokens 27.7 us on 128 x 256
-    // against 30.2 fused, at 2400 tokens 38.4 on 192 x 256 against 39.7.
-    const int tiles[3] = {kF16T256x256, kF16T192x256, kF16T128x256}, charge[3] = {1000, 904, 650};
+    // against 30.2 fused, at 2400 tokens 38.4 on 192 x 256 against 39.7;
+    // Q6_K 2048 x 8192 in 4 splits at 500 tokens 35.7 on 128 x 128, 41.5 on
+    // 128 x 256.
+    const int tiles[4] = {kF16T256x256, kF16T192x256, kF16T128x256, kF16T128x128};
+    const int charge[4] = {1000, 904, 650, 380};
     int best = kF16None, cost = 0;
-    for (int i = 0; i < 3; ++i) {
-      const int wg = ((m + f16_bm(tiles[i]) - 1) / f16_bm(tiles[i])) * (w.n / 256) * splits;
+    for (int i = 0; i < 4; ++i) {
+      const int wg = ((m + f16_bm(tiles[i]) - 1) / f16_bm(tiles[i])) * (w.n / f16_bn(tiles[i])) * splits;
       const int c = charge[i] * ((wg + 255) / 256);
       if (best == kF16None || c < cost) best = tiles[i], cost = c;
     }
     return best;
   }
   if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) {
-    // 128-row tiles when 256-row tiles leave CUs without a workgroup and
-    // 128 x 128 tiles would not: 128 x 256 on 8 waves where the columns
-    // allow, else 128 x 128 on 4 waves (the QKV projection's f16 GEMM at
-    // 1536 tokens: 34.9 us on 144 workgroups of 128 x 256, 36.4 on 288 of
-    // 128 x 128; at 2400 tokens 39.4 and 40.6).
-    if (mt * (w.n / 128) < 256 && ((m + 127) / 128) * (w.n / 128) >= 256)
-      return w.n % 256 == 0 ? kF16T128x256 : kF16T128x128;
+    // 128-row tiles: 128 x 256 on 8 waves where the columns allow (the QKV
+    // projection's f16 GEMM at 1536 tokens: 34.9 us on 144 workgroups of
+    // 128 x 256, 36.4 on 288 of 128 x 128; at 2400 tokens 39.4 and 40.6;
+    // gate/up at 320 tokens 48.8 with its expansion against 55.1 on 256 x
+    // 128), else 128 x 128 on 4 waves when 256-row tiles leave CUs without a
+    // workgroup and 128-row tiles do not, else 256 x 128.
+    if (w.n % 256 == 0) return kF16T128x256;
+    if (mt * (w.n / 128) < 256 && ((m + 127) / 128) * (w.n / 128) >= 256) return kF16T128x128;
     return kF16T256x128;
   }
   return kF16None;
