@@ -491,10 +491,10 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
 // WM waves along M (32 MI rows each) x BN/128 along N (128 columns each).
 // LDS: two stages of the BM x 64 X tile and the BN x 64 W tile (128 bytes
 // per row). Configurations: 256 x 256 (8 waves of 64 x 128), 256 x 128 (4
-// waves of 64 x 128), 192 x 256 and 128 x 256 (4 waves of 96 or 64 x 128):
-// the tile grid is chosen per problem so the last round of workgroups is as
-// full as possible, and every configuration issues the same MFMA sequence
-// per output element.
+// waves of 64 x 128), 192 x 256 (4 waves of 96 x 128), 128 x 256 (8 waves of
+// 32 x 128) and 128 x 128 (4 waves of 32 x 128): the tile grid is chosen per
+// problem by counting rounds of 256 workgroups, and every configuration
+// issues the same MFMA sequence per output element.
 constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
 
 template <int EPI, int BN, int WM, int MI>
@@ -719,17 +719,19 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     }
     return best;
   }
-  if (splits > 1 && w.n % 256 == 0) {
-    // K split over too few column tiles for a round of 256-row tiles: the
+  if (w.n % 256 == 0 && (splits > 1 || mt * (w.n / 128) >= 64)) {
+    // Too few column tiles (or K split) for a round of 256-row tiles: the
     // tiling with the fewest rounds of 256 workgroups, a round charged its
     // tiles' relative time (256 rows 1000, 192 rows 904, 128 rows 650,
-    // 128 x 128 380).
-    // Measured (expansion included): Q6_K 2048 x 8192 in 2 splits at 2400
-    // tokens 101.8 us on 192 x 256 (256 x 256 105.8) against 140.8 fused;
-    // Q4_K 2048 x 2048 in 2 splits at 1536 tokens 27.7 us on 128 x 256
-    // against 30.2 fused, at 2400 tokens 38.4 on 192 x 256 against 39.7;
-    // Q6_K 2048 x 8192 in 4 splits at 500 tokens 35.7 on 128 x 128, 41.5 on
-    // 128 x 256.
+    // 128 x 128 380). Measured (expansion included): Q6_K 2048 x 8192 in 2
+    // splits at 2400 tokens 101.8 us on 192 x 256 (256 x 256 105.8) against
+    // 140.8 fused; Q4_K 2048 x 2048 in 2 splits at 1536 tokens 27.7 on
+    // 128 x 256 against 30.2 fused, at 2400 tokens 38.4 on 192 x 256
+    // against 39.7; Q6_K 2048 x 8192 in 4 splits at 500 tokens 35.7 on
+    // 128 x 128, 41.5 on 128 x 256; Q4_0 12288 x 2048 at 800 tokens 68.4 on
+    // 192 x 256 (128 x 256 81.0), at 1024 tokens 72.3 on 256 x 256; the QKV
+    // projection's f16 GEMM at 1536 tokens 34.9 on 128 x 256 against 36.4 on
+    // 128 x 128.
     const int tiles[4] = {kF16T256x256, kF16T192x256, kF16T128x256, kF16T128x128};
     const int charge[4] = {1000, 904, 650, 380};
     int best = kF16None, cost = 0;
@@ -741,13 +743,8 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     return best;
   }
   if (splits == 1 && w.n % 128 == 0 && mt * (w.n / 128) >= 64) {
-    // 128-row tiles: 128 x 256 on 8 waves where the columns allow (the QKV
-    // projection's f16 GEMM at 1536 tokens: 34.9 us on 144 workgroups of
-    // 128 x 256, 36.4 on 288 of 128 x 128; at 2400 tokens 39.4 and 40.6;
-    // gate/up at 320 tokens 48.8 with its expansion against 55.1 on 256 x
-    // 128), else 128 x 128 on 4 waves when 256-row tiles leave CUs without a
-    // workgroup and 128-row tiles do not, else 256 x 128.
-    if (w.n % 256 == 0) return kF16T128x256;
+    // Columns in 128s only: 128 x 128 tiles on 4 waves when 256-row tiles
+    // leave CUs without a workgroup and 128-row tiles do not, else 256 x 128.
     if (mt * (w.n / 128) < 256 && ((m + 127) / 128) * (w.n / 128) >= 256) return kF16T128x128;
     return kF16T256x128;
   }
