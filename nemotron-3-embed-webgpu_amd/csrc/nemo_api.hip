@@ -280,6 +280,7 @@ struct nemo_plan {
   hipStream_t stream = nullptr;
   std::mutex mu;
   DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, attn, delta, ffn, out, rope, partials, wexp;
+  size_t wexp_halves = 0;
   // Rows of the last layer run (the attention's RoPE positions) and, made
   // on request, its rotated query and key heads.
   Ragged last_rows{};
@@ -665,6 +666,15 @@ static std::vector<float> rope_table(int sequence, int head_dim, double theta) {
   return v;
 }
 
+// Whether a pass of m tokens expands a layer's QKV and O weights to f16 in
+// one launch before the QKV projection (both single Q4_K matrices on the
+// two-pass path; each expansion alone is latency-bound: 5.6 and 5.3 us at
+// the benchmark dims).
+static bool expand_qkv_o_together(const LayerWeights& w, int m) {
+  return m > kGemvMaxM && w.qkv_parts.empty() && w.qkv.type == kQ4_K && w.o.type == kQ4_K &&
+         gemm_two_pass(w.qkv, m, gemm_splits(w.qkv, m)) && gemm_two_pass(w.o, m, gemm_splits(w.o, m));
+}
+
 nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence, nemo_plan** out) {
   return guarded([&] {
     if (!model || !out) fail(NEMO_ERR_INVALID, "null argument");
@@ -731,12 +741,16 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     for (const LayerWeights& w : model->layers) {
       std::vector<const QWeight*> mats = qkv_matrices(w);
       mats.insert(mats.end(), {&w.o, &w.gate_up, &w.down});
-      for (const QWeight* q : mats)
-        for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)})
+      for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)}) {
+        for (const QWeight* q : mats)
           if (gemm_two_pass(*q, (int)m, gemm_splits(*q, (int)m)))
             wexp_halves = std::max(wexp_halves, (size_t)q->n * q->k);
+        if (expand_qkv_o_together(w, (int)m))
+          wexp_halves = std::max(wexp_halves, (size_t)w.qkv.n * w.qkv.k + (size_t)w.o.n * w.o.k);
+      }
     }
     if (wexp_halves) p->wexp = dev_alloc(wexp_halves * 2, "f16 weight expansion");
+    p->wexp_halves = wexp_halves;
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
     const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
     p->rope = dev_alloc(table.size() * 4, "RoPE sin/cos table");
@@ -872,15 +886,23 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // depend on the pass size, so within a regime a token's result does not
     // depend on the rest of the batch.
     const bool small = M <= kGemvMaxM;
+    // QKV and O expanded together: QKV at wexp, O after it.
+    const bool pair = expand_qkv_o_together(w, M) &&
+                      (size_t)w.qkv.n * w.qkv.k + (size_t)w.o.n * w.o.k <= p->wexp_halves;
+    uint16_t* wexp_o = pair ? wexp + (size_t)w.qkv.n * w.qkv.k : wexp;
+    if (pair)
+      hip_check(launch_expand_q4k_pair(w.qkv.blocks, (int64_t)w.qkv.n * (w.qkv.k / 256), wexp, w.o.blocks,
+                                       (int64_t)w.o.n * (w.o.k / 256), wexp_o, s),
+                "qkv/o expansion");
     // One matrix, or separate q / k / v parts each into its column range.
     auto qkv_proj = [&](const QWeight& wq, int col) {
       const int sp = gemm_splits(wq, M);
       if (small) {
         hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
       } else if (sp == 1) {
-        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp), "qkv matmul");
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp, pair), "qkv matmul");
       } else {
-        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s, wexp), "qkv matmul");
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s, wexp, pair), "qkv matmul");
         hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
       }
     };
@@ -901,7 +923,8 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     mark(3, false);
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
-    auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage) {
+    auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage,
+                        uint16_t* wx, bool expanded) {
       const int splits = small ? gemv_splits(wt) : gemm_splits(wt, M);
       mark(stage, true);
       if (small)
@@ -909,9 +932,10 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
                                  splits == 1 ? (void*)delta : (void*)partials, H, nullptr, s),
                   "residual gemv");
       else if (splits == 1)
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wexp), "residual matmul");
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wx, expanded), "residual matmul");
       else
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wexp), "residual matmul");
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wx, expanded),
+                  "residual matmul");
       mark(stage, false);
       mark(stage + 1, true);
       if (splits == 1)
@@ -920,7 +944,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
         hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
       mark(stage + 1, false);
     };
-    residual(attn, QW, w.o, w.ffn_norm, 4);
+    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
     if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
@@ -929,7 +953,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     }
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
-    residual(ffn, F, w.down, next, 8);
+    residual(ffn, F, w.down, next, 8, wexp, false);
   }
   if (d.merge_after_layer == d.layers) {  // merge after the last layer (models shorter than the reference)
     mark(1, true);

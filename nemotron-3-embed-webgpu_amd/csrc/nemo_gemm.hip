@@ -773,12 +773,15 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
 }
 
 static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
-                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream, int tile) {
+                                  void* out, int ldo, uint16_t* wexp, hipStream_t stream, int tile,
+                                  bool expanded = false) {
   const int bm = f16_bm(tile), bn = f16_bn(tile);
   if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
-  if (w.type == kQ4_K) {
+  if (expanded) {
+    // wexp already holds the expansion
+  } else if (w.type == kQ4_K) {
     // GGUF Q4_K rows are whole blocks: the row-major f16 matrix is the
     // blocks' decode in order (full-line stores, same values).
     const hipError_t e = launch_expand_q4k(w.blocks, (int64_t)w.n * (w.k / 256), wexp, stream);
@@ -812,7 +815,8 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
 }
 
 static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
-                               void* out, int ldo, hipStream_t stream, uint16_t* wexp, int forced) {
+                               void* out, int ldo, hipStream_t stream, uint16_t* wexp, int forced,
+                               bool expanded = false) {
   if (m <= 0) return hipSuccess;
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
   if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
@@ -821,7 +825,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   const int kchunk = w.k / splits;
   if (forced < 0 && use_mid(w, m, splits)) forced = kVarMid;
   const int tile = (wexp && forced < 0) ? two_pass_tile(w, m, splits) : kF16None;
-  if (tile != kF16None) return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile);
+  if (tile != kF16None)
+    return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile, expanded);
   const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
 #define NEMO_LAUNCH(T)                                                                                              \
   if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
@@ -839,8 +844,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
 }
 
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream, uint16_t* wexp) {
-  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, wexp, -1);
+                          int ldo, hipStream_t stream, uint16_t* wexp, bool expanded) {
+  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, wexp, -1, expanded);
 }
 
 hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,

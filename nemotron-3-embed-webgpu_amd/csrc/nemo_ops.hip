@@ -270,7 +270,7 @@ hipError_t launch_rope(const uint16_t* qkv, int qkv_stride, const Ragged& rows, 
 // keys a lane holds (the key order of a sum is free; A and B agree on it).
 // ---------------------------------------------------------------------------
 
-constexpr int kAttnQ = 32, kAttnKeys = 32, kVtPad = 40;
+constexpr int kAttnQ = 32, kAttnKeys = 32;
 
 __device__ __forceinline__ int attn_keys(int n, int stride_threshold, int key_stride_long) {
   const int s = n > stride_threshold ? key_stride_long : 1;

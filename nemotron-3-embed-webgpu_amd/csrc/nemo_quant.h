@@ -65,9 +65,15 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 
 // The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial. With
 // `wexp` (room for n * k halves) large problems take the two-pass path, whose
-// results are bit-identical to the fused kernels'.
+// results are bit-identical to the fused kernels'. `expanded`: wexp already
+// holds w's f16 expansion (launch_expand_q4k_pair), which the two-pass path
+// then uses as it is.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream, uint16_t* wexp = nullptr);
+                          int ldo, hipStream_t stream, uint16_t* wexp = nullptr, bool expanded = false);
+// Two Q4_K matrices' blocks -> f16, row-major, in one launch (each alone
+// would be latency-bound): n0 blocks of blocks0 to out0, n1 of blocks1 to out1.
+hipError_t launch_expand_q4k_pair(const uint8_t* blocks0, int64_t n0, uint16_t* out0, const uint8_t* blocks1,
+                                  int64_t n1, uint16_t* out1, hipStream_t stream);
 // A matrix's blocks regrouped for the GEMV (n % 16 == 0): per 16-row tile
 // and 256 values, the bytes each lane group of a GEMV wave loads sit
 // side by side for the 16 rows, so every load of the wave reads whole

@@ -547,14 +547,12 @@ hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
 // bytes (f16) or 256 (f32): the low nibbles of bytes 8c .. 8c + 8 of every
 // group's 32 (c < 4) or the high nibbles of bytes 8(c - 4) .. (c >= 4).
 // NT: non-temporal stores, for output that is not read back soon.
+// Thread c (0..7) of the 144-byte block at `blk`, whose values start at
+// element o of the outputs.
 template <bool NT>
-__global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restrict__ raw, int64_t n_blocks,
-                                                          float* __restrict__ out32, uint16_t* __restrict__ out16) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t b = t >> 3;
-  if (b >= n_blocks) return;
-  const int c = (int)(t & 7), part = c & 3, high = c >> 2;
-  const uint8_t* blk = raw + b * 144;
+__device__ __forceinline__ void q4k_block_part(const uint8_t* __restrict__ blk, int c, int64_t o0,
+                                               float* __restrict__ out32, uint16_t* __restrict__ out16) {
+  const int part = c & 3, high = c >> 2;
   const u32x4 hdr = *(const u32x4*)blk;
   uint32_t q[4][2];
 #pragma unroll
@@ -572,7 +570,7 @@ __global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restr
     float v[8];
     bytes4_fma(opaque((q[i][0] >> sh) & 0x0f0f0f0fu), dsc, ndm, v);
     bytes4_fma(opaque((q[i][1] >> sh) & 0x0f0f0f0fu), dsc, ndm, v + 4);
-    const int64_t o = b * 256 + 64 * i + 8 * c;
+    const int64_t o = o0 + 64 * i + 8 * c;
     if constexpr (NT) {
       if (out32) {
         __builtin_nontemporal_store(float4v{v[0], v[1], v[2], v[3]}, (float4v*)(out32 + o));
@@ -587,6 +585,38 @@ __global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restr
       if (out16) *(half8v*)(out16 + o) = to_half8(v);
     }
   }
+}
+
+template <bool NT>
+__global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restrict__ raw, int64_t n_blocks,
+                                                          float* __restrict__ out32, uint16_t* __restrict__ out16) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = t >> 3;
+  if (b >= n_blocks) return;
+  q4k_block_part<NT>(raw + b * 144, (int)(t & 7), b * 256, out32, out16);
+}
+
+// Two matrices in one launch: blocks [0, n0) of raw0 to out0, then the n1 of
+// raw1 to out1 (f16, row-major; small expansions are latency-bound alone).
+__global__ __launch_bounds__(256) void expand_q4k_pair_kernel(const uint8_t* __restrict__ raw0, int64_t n0,
+                                                              uint16_t* __restrict__ out0,
+                                                              const uint8_t* __restrict__ raw1, int64_t n1,
+                                                              uint16_t* __restrict__ out1) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t b = t >> 3;
+  if (b < n0) {
+    q4k_block_part<false>(raw0 + b * 144, (int)(t & 7), b * 256, nullptr, out0);
+  } else if ((b -= n0) < n1) {
+    q4k_block_part<false>(raw1 + b * 144, (int)(t & 7), b * 256, nullptr, out1);
+  }
+}
+
+hipError_t launch_expand_q4k_pair(const uint8_t* blocks0, int64_t n0, uint16_t* out0, const uint8_t* blocks1,
+                                  int64_t n1, uint16_t* out1, hipStream_t stream) {
+  if (n0 + n1 <= 0) return hipSuccess;
+  expand_q4k_pair_kernel<<<(unsigned)(((n0 + n1) * 8 + 255) / 256), 256, 0, stream>>>(blocks0, n0, out0, blocks1, n1,
+                                                                                        out1);
+  return hipGetLastError();
 }
 
 hipError_t launch_expand_q4k(const uint8_t* blocks, int64_t n_blocks, uint16_t* out16, hipStream_t stream) {
