@@ -53,9 +53,16 @@ mean_pool                      unit norm; a single repeated row -> its
 matmul                         fp64 dot of the reference CPU check
                                (src/main.ts:97-109) on integer-valued inputs
                                where float64 is exact
-forward                        batch composition invariance and the pins of
-                               its parts; end-to-end values are compared with
-                               the HIP path only by tolerance (cosine)
+forward / forward_request      graph wiring (src/webgpu/model.ts:113-138,
+                               154-168) by closed forms: zero projections ->
+                               pool of the output-normalized merged rows;
+                               power-of-two norm weights -> which norm follows
+                               which residual add; a value-passthrough layer
+                               after the merge -> the normalized stream is
+                               merged as it is; RoPE positions restart after
+                               the merge; each pin fails on a planted wiring
+                               mistake (tests/test_oracle_wiring*.py); batch
+                               composition invariance
 =============================  ==============================================
 """
 from __future__ import annotations
