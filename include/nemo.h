@@ -130,7 +130,8 @@ nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, co
 
 /* Same graph with ids and out as device pointers, enqueued on `stream`
  * (hipStream_t; NULL = the plan's own stream); lengths are host values.
- * Returns once enqueued. */
+ * Returns once enqueued. Work of the plan enqueued earlier on another stream
+ * is waited for on the device first (the runs share the plan's buffers). */
 nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const uint32_t* lengths, size_t n_lengths,
                                  float* d_out, void* stream);
 
@@ -141,8 +142,18 @@ nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids
 int32_t nemo_profile_stage_count(void);
 const char* nemo_profile_stage_name(int32_t index);
 
-/* destroy() (src/webgpu/model.ts:141-144). */
+/* destroy() (src/webgpu/model.ts:141-144). Waits for a call on the plan
+ * that another thread is running, then for all work the plan enqueued (on
+ * its own stream or a caller's), then frees it. The caller must not start
+ * further calls on the plan, nor have any waiting to start: the host
+ * bindings count their runs in flight and destroy once the last settles. */
 nemo_status nemo_plan_destroy(nemo_plan* plan);
+
+/* The plan's batch, sequence and the model's hidden width (any pointer may
+ * be NULL): a binding sizes the embeddings of a run, batch * hidden floats,
+ * from the plan itself. No counterpart in the reference, whose plan object
+ * carries these fields (src/webgpu/model.ts:58-74). */
+nemo_status nemo_plan_shape(nemo_plan* plan, int32_t* batch, int32_t* sequence, int32_t* hidden);
 
 /* Copy one activation buffer of the last run to the host, for stage-wise
  * parity checks (the reference's buffers of src/webgpu/model.ts:80-94 are

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -261,7 +262,7 @@ struct nemo_model {
   const float* output_norm = nullptr;
   int embedding_type = -1;
   const void* embedding = nullptr;
-  int live_plans = 0;
+  std::atomic<int> live_plans{0};  // plans are created and destroyed from any thread
 };
 
 struct nemo_weight {
@@ -291,12 +292,34 @@ struct nemo_plan {
   int attn_keys_cap = 0;
   uint32_t* h_ids = nullptr;   // pinned staging
   float* h_out = nullptr;
+  // Recorded after every enqueue of the plan's work, on the stream it went
+  // to (last_stream): the next enqueue on another stream, read_buffer and
+  // destroy wait for it, since every run of the plan shares its buffers.
+  hipEvent_t done = nullptr;
+  hipStream_t last_stream = nullptr;
   ~nemo_plan() {
     if (h_ids) (void)hipHostFree(h_ids);
     if (h_out) (void)hipHostFree(h_out);
+    if (done) (void)hipEventDestroy(done);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
+
+// Every enqueue of a plan's work is bracketed by these (plan->mu held): work
+// on a stream other than the last one first waits for the plan's previous
+// work, and the event then marks the end of the new work.
+static void plan_begin(nemo_plan* p, hipStream_t s) {
+  if (p->last_stream && p->last_stream != s) hip_check(hipStreamWaitEvent(s, p->done, 0), "hipStreamWaitEvent");
+}
+static void plan_end(nemo_plan* p, hipStream_t s) {
+  hip_check(hipEventRecord(p->done, s), "hipEventRecord");
+  p->last_stream = s;
+}
+// Blocks until all of the plan's enqueued work, on any stream, is done.
+static void plan_wait(nemo_plan* p) {
+  if (p->last_stream) hip_check(hipEventSynchronize(p->done), "hipEventSynchronize");
+  if (p->stream) hip_check(hipStreamSynchronize(p->stream), "hipStreamSynchronize");
+}
 
 static void set_device(nemo_ctx* ctx) { hip_check(hipSetDevice(ctx->device), "hipSetDevice"); }
 
@@ -692,6 +715,7 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     const size_t H = d.hidden, QKV = (size_t)(d.q_heads + 2 * d.kv_heads) * d.head_dim;
     const size_t QW = (size_t)d.q_heads * d.head_dim, F = d.intermediate;
     hip_check(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking), "hipStreamCreate");
+    hip_check(hipEventCreateWithFlags(&p->done, hipEventDisableTiming), "hipEventCreate");
     p->ids = dev_alloc(tf * 4, "token ids");
     p->x_full = dev_alloc(tf * H * 2, "full residual stream");
     p->norm_full = dev_alloc(tf * H * 2, "full normalized hidden state");
@@ -765,10 +789,24 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
 nemo_status nemo_plan_destroy(nemo_plan* plan) {
   return guarded([&] {
     if (!plan) return;
-    set_device(plan->model->ctx);
-    if (plan->stream) hip_check(hipStreamSynchronize(plan->stream), "sync");
+    {
+      // A run, profile or read of the plan on another thread finishes first
+      // (it holds the lock), then everything the plan enqueued, on any stream.
+      std::lock_guard<std::mutex> lock(plan->mu);
+      set_device(plan->model->ctx);
+      plan_wait(plan);
+    }
     plan->model->live_plans--;
     delete plan;
+  });
+}
+
+nemo_status nemo_plan_shape(nemo_plan* plan, int32_t* batch, int32_t* sequence, int32_t* hidden) {
+  return guarded([&] {
+    if (!plan) fail(NEMO_ERR_INVALID, "null argument");
+    if (batch) *batch = plan->batch;
+    if (sequence) *sequence = plan->sequence;
+    if (hidden) *hidden = plan->model->dims.hidden;
   });
 }
 
@@ -784,6 +822,7 @@ nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, 
     const std::string n = name;
     const void* src = nullptr;
     size_t bytes = 0;
+    if (out) plan_wait(plan);  // the last run may have gone to a caller's stream
     if (n == "x_full") src = plan->x_full.get(), bytes = tf * H * 2;
     else if (n == "norm_full") src = plan->norm_full.get(), bytes = tf * H * 2;
     else if (n == "x_merged") src = plan->x_red.get(), bytes = tr * H * 2;
@@ -811,7 +850,6 @@ nemo_status nemo_plan_read_buffer(nemo_plan* plan, const char* name, void* out, 
     }
     if (*n_bytes < bytes) fail(NEMO_ERR_INVALID, "output buffer too small");
     hip_check(hipStreamSynchronize(plan->stream), "sync");
-    hip_check(hipDeviceSynchronize(), "sync");
     hip_check(hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost), "download");
     *n_bytes = bytes;
   });
@@ -986,11 +1024,13 @@ nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, co
     check_ids_host(plan, ids, n_ids, src);
     const size_t H = plan->model->dims.hidden;
     hipStream_t s = plan->stream;
+    plan_begin(plan, s);
     memcpy(plan->h_ids, ids, n_ids * 4);
     hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
     enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s, [](int, bool) {});
     hip_check(hipMemcpyAsync(plan->h_out, plan->out.get(), (size_t)plan->batch * H * 4, hipMemcpyDeviceToHost, s),
               "readback");
+    plan_end(plan, s);
     hip_check(hipStreamSynchronize(s), "run");
     memcpy(out, plan->h_out, (size_t)plan->batch * H * 4);
   });
@@ -1005,7 +1045,9 @@ nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const u
     Ragged src, dst;
     ragged_tables(plan, lengths, n_lengths, src, dst);
     hipStream_t s = stream ? (hipStream_t)stream : plan->stream;
+    plan_begin(plan, s);
     enqueue_graph(plan, d_ids, src, dst, d_out, s, [](int, bool) {});
+    plan_end(plan, s);
   });
 }
 
@@ -1019,6 +1061,7 @@ nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids
     ragged_tables(plan, lengths, n_lengths, src, dst);
     check_ids_host(plan, ids, n_ids, src);
     hipStream_t s = plan->stream;
+    plan_begin(plan, s);
     memcpy(plan->h_ids, ids, n_ids * 4);
     hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
     // One event pair per stage instance, like the reference's one timestamp
@@ -1038,6 +1081,7 @@ nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids
                       ++next;
                     }
                   });
+    plan_end(plan, s);
     hip_check(hipStreamSynchronize(s), "profile");
     for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
     for (int i = 0; i < next; ++i) {

@@ -94,7 +94,13 @@ function asU32(values) {
   return values instanceof Uint32Array ? values : Uint32Array.from(values);
 }
 
-/** NemotronExecutionPlan (src/webgpu/model.ts:58-234). */
+/**
+ * NemotronExecutionPlan (src/webgpu/model.ts:58-234). Runs in flight are
+ * counted: destroy() while some are pending closes the plan to new calls at
+ * once and frees it when the last settles, so a pending run resolves
+ * normally (WebGPU's destroy() is likewise safe with queued work,
+ * src/webgpu/model.ts:141-144). The addon enforces the same on its handle.
+ */
 class NemotronHipPlan {
   constructor(model, batch, inputSequence) {
     this.model = model;
@@ -102,26 +108,40 @@ class NemotronHipPlan {
     this.inputSequence = inputSequence;
     this.sequence = contextualMergedLength(inputSequence);
     this.handle = native().planCreate(model.handle, batch, inputSequence);
+    this.pending = 0;
+    this.closed = false;
+    this.destroyed = false;
   }
 
   /** src/webgpu/model.ts:146-176: batch fresh Float32Array(hidden), in input order. */
   run(ids, sequenceLengths) {
-    const hidden = this.model.dims.hidden;
+    if (this.closed) return Promise.reject(new Error('plan was destroyed'));
     let pending;
     try {
-      pending = native().planRun(this.handle, asU32(ids), asU32(sequenceLengths), hidden);
+      pending = native().planRun(this.handle, asU32(ids), asU32(sequenceLengths));
     } catch (error) {
       return Promise.reject(error);
     }
+    this.pending += 1;
+    const settle = () => {
+      this.pending -= 1;
+      if (this.closed && this.pending === 0) this.free();
+    };
     return pending.then((flat) => {
+      settle();
+      const hidden = flat.length / this.batch;
       const out = [];
       for (let b = 0; b < this.batch; b += 1) out.push(flat.slice(b * hidden, (b + 1) * hidden));
       return out;
+    }, (error) => {
+      settle();
+      throw error;
     });
   }
 
   /** src/webgpu/model.ts:178-224: milliseconds per stage name, summed over layers. */
   profile(ids, sequenceLengths) {
+    if (this.closed) return Promise.reject(new Error('plan was destroyed'));
     try {
       return Promise.resolve(native().planProfile(this.handle, asU32(ids), asU32(sequenceLengths)));
     } catch (error) {
@@ -131,8 +151,15 @@ class NemotronHipPlan {
 
   /** src/webgpu/model.ts:141-144. Later calls on the plan fail with 'plan was destroyed'. */
   destroy() {
-    if (!this.destroyed) native().planDestroy(this.handle);
+    if (this.closed) return;
+    this.closed = true;
+    if (this.pending === 0) this.free();
+  }
+
+  free() {
+    if (this.destroyed) return;
     this.destroyed = true;
+    native().planDestroy(this.handle);
   }
 }
 

@@ -2,12 +2,16 @@
  * the JavaScript host (js/runtime.js), replacing the WebGPU calls of
  * src/webgpu/model.ts and src/webgpu/device.ts.
  *
- * Handles are externals wrapping a pointer that destroy() clears, so a use
- * after destroy throws instead of touching freed memory. planRun executes
- * nemo_plan_run on the libuv thread pool (napi_async_work) and settles a
- * Promise, like EmbeddingPlan.run (src/webgpu/embedding-engine.ts:8); distinct
- * plans may run concurrently, runs of one plan are serialised by libnemo.
- * Every failure becomes a JS Error carrying nemo_last_error(). */
+ * Handles are externals wrapping a pointer. planRun executes nemo_plan_run on
+ * the libuv thread pool (napi_async_work) and settles a Promise, like
+ * EmbeddingPlan.run (src/webgpu/embedding-engine.ts:8); distinct plans may
+ * run concurrently, runs of one plan are serialised by libnemo. A plan handle
+ * counts its runs in flight: planDestroy closes it to new calls at once
+ * (they throw 'plan was destroyed') and frees the plan when the last run has
+ * settled, on the JS thread, so a pending run resolves normally (WebGPU's
+ * destroy() is likewise safe with work already queued,
+ * src/webgpu/model.ts:141-144). Every failure becomes a JS Error carrying
+ * nemo_last_error(). */
 #include <node_api.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -26,7 +30,9 @@
 
 typedef struct {
   void* ptr;
-  int kind; /* 1 ctx, 2 model, 3 plan */
+  int kind;    /* 1 ctx, 2 model, 3 plan */
+  int pending; /* plan runs queued or executing (touched on the JS thread only) */
+  int closed;  /* planDestroy was called; the plan is freed once pending is 0 */
 } handle_t;
 
 static const char* kKindName[] = {"", "context", "model", "plan"};
@@ -46,6 +52,8 @@ static napi_value wrap(napi_env env, void* ptr, int kind) {
   }
   h->ptr = ptr;
   h->kind = kind;
+  h->pending = 0;
+  h->closed = 0;
   if (napi_create_external(env, h, handle_finalize, NULL, &out) != napi_ok) {
     free(h);
     napi_throw_error(env, NULL, "cannot create handle");
@@ -64,7 +72,7 @@ static handle_t* unwrap(napi_env env, napi_value v, int kind) {
     napi_throw_type_error(env, NULL, msg);
     return NULL;
   }
-  if (!h->ptr) {
+  if (!h->ptr || h->closed) {
     char msg[64];
     snprintf(msg, sizeof msg, "%s was destroyed", kKindName[kind]);
     napi_throw_error(env, NULL, msg);
@@ -344,6 +352,8 @@ static napi_value js_plan_destroy(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, argv)) return NULL;
   handle_t* h = unwrap(env, argv[0], 3);
   if (!h) return NULL;
+  h->closed = 1;
+  if (h->pending > 0) return undefined(env); /* freed by the last run_complete */
   nemo_status s = nemo_plan_destroy((nemo_plan*)h->ptr);
   h->ptr = NULL;
   if (s) return throw_status(env, s);
@@ -356,6 +366,7 @@ typedef struct {
   napi_async_work work;
   napi_deferred deferred;
   napi_ref plan_ref; /* keeps the plan handle alive while the work runs */
+  handle_t* handle;
   nemo_plan* plan;
   uint32_t* ids;
   size_t n_ids;
@@ -402,6 +413,13 @@ static void run_complete(napi_env env, napi_status status, void* data) {
       napi_reject_deferred(env, j->deferred, err);
     }
   }
+  /* On the JS thread, before the handle may be collected: a destroy that
+   * arrived while runs were in flight frees the plan after the last. */
+  handle_t* h = j->handle;
+  if (--h->pending == 0 && h->closed && h->ptr) {
+    (void)nemo_plan_destroy((nemo_plan*)h->ptr);
+    h->ptr = NULL;
+  }
   napi_delete_reference(env, j->plan_ref);
   napi_delete_async_work(env, j->work);
   free(j->ids);
@@ -410,28 +428,31 @@ static void run_complete(napi_env env, napi_status status, void* data) {
   free(j);
 }
 
-/* planRun(plan, ids: Uint32Array, lengths: Uint32Array, hidden) ->
- * Promise<Float32Array(batch * hidden)>. ids and lengths are copied at the
- * call, as the reference writes them into its buffers (model.ts:149-151). */
+/* planRun(plan, ids: Uint32Array, lengths: Uint32Array) ->
+ * Promise<Float32Array(batch * hidden)>, batch and hidden taken from the
+ * native plan (nemo_plan_shape). ids and lengths are copied at the call, as
+ * the reference writes them into its buffers (model.ts:149-151). */
 static napi_value js_plan_run(napi_env env, napi_callback_info info) {
-  napi_value argv[4], promise, name;
+  napi_value argv[3], promise, name;
   const uint32_t *ids, *lengths;
   size_t n_ids, n_lengths;
-  int32_t hidden;
-  if (!get_args(env, info, 4, argv)) return NULL;
+  int32_t batch = 0, hidden = 0;
+  if (!get_args(env, info, 3, argv)) return NULL;
   handle_t* h = unwrap(env, argv[0], 3);
-  if (!h || !get_u32_array(env, argv[1], &ids, &n_ids) || !get_u32_array(env, argv[2], &lengths, &n_lengths) ||
-      !get_i32(env, argv[3], &hidden))
+  if (!h || !get_u32_array(env, argv[1], &ids, &n_ids) || !get_u32_array(env, argv[2], &lengths, &n_lengths))
     return NULL;
+  nemo_status st = nemo_plan_shape((nemo_plan*)h->ptr, &batch, NULL, &hidden);
+  if (st) return throw_status(env, st);
   run_job_t* j = (run_job_t*)calloc(1, sizeof(run_job_t));
   if (!j) {
     napi_throw_error(env, NULL, "out of host memory");
     return NULL;
   }
+  j->handle = h;
   j->plan = (nemo_plan*)h->ptr;
   j->n_ids = n_ids;
   j->n_lengths = n_lengths;
-  j->n_out = n_lengths * (size_t)(hidden > 0 ? hidden : 0);
+  j->n_out = (size_t)batch * (size_t)hidden;
   j->ids = (uint32_t*)malloc(n_ids * 4 + 4);
   j->lengths = (uint32_t*)malloc(n_lengths * 4 + 4);
   j->out = (float*)malloc(j->n_out * 4 + 4);
@@ -450,6 +471,7 @@ static napi_value js_plan_run(napi_env env, napi_callback_info info) {
   CHECK_NAPI(env, napi_create_string_utf8(env, "nemo_plan_run", NAPI_AUTO_LENGTH, &name));
   CHECK_NAPI(env, napi_create_async_work(env, NULL, name, run_execute, run_complete, j, &j->work));
   CHECK_NAPI(env, napi_queue_async_work(env, j->work));
+  h->pending++;
   return promise;
 }
 

@@ -24,7 +24,7 @@ EXPORTED = [
     "nemo_model_create", "nemo_model_set_tensor", "nemo_model_synthesize", "nemo_model_finalize",
     "nemo_model_get_tensor", "nemo_model_destroy", "nemo_plan_create", "nemo_plan_run", "nemo_plan_run_device",
     "nemo_plan_profile", "nemo_profile_stage_count", "nemo_profile_stage_name", "nemo_plan_destroy",
-    "nemo_plan_read_buffer",
+    "nemo_plan_shape", "nemo_plan_read_buffer",
     "nemo_weight_create", "nemo_weight_destroy", "nemo_weight_matmul", "nemo_weight_dequantize", "nemo_dequantize",
     "nemo_requantize_q40",
 ]
@@ -83,6 +83,7 @@ def load() -> ctypes.CDLL:
         "nemo_profile_stage_count": (i32, []),
         "nemo_profile_stage_name": (ctypes.c_char_p, [i32]),
         "nemo_plan_destroy": (i32, [vp]),
+        "nemo_plan_shape": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)]),
         "nemo_plan_read_buffer": (i32, [vp, ctypes.c_char_p, vp, ctypes.POINTER(sz)]),
         "nemo_weight_create": (i32, [vp, i32, i32, i32, vp, sz, pp]),
         "nemo_weight_destroy": (i32, [vp]),

@@ -14,6 +14,7 @@ from __future__ import annotations
 import asyncio
 import ctypes
 import math
+import threading
 from typing import Iterable
 
 import numpy as np
@@ -80,7 +81,13 @@ def _u32(a) -> np.ndarray:
 
 class NemotronHipPlan:
     """An execution plan for `batch` requests of up to `sequence` tokens
-    (NemotronExecutionPlan, src/webgpu/model.ts:58-234)."""
+    (NemotronExecutionPlan, src/webgpu/model.ts:58-234).
+
+    Runs in flight are counted: ``destroy()`` while some are pending closes
+    the plan to new calls at once and frees it when the last one settles,
+    so a pending run resolves normally (WebGPU's destroy() is likewise safe
+    with work already queued, src/webgpu/model.ts:141-144).
+    """
 
     def __init__(self, model: "NemotronHipModel", batch: int, sequence: int):
         self.model = model
@@ -88,32 +95,77 @@ class NemotronHipPlan:
         self.inputSequence = sequence
         self.sequence = contextual_merged_length(sequence)
         self._ptr = ctypes.c_void_p()
+        self._lock = threading.Lock()
+        self._pending = 0
+        self._closed = False
         check(_lib.load().nemo_plan_create(model.ptr, batch, sequence, ctypes.byref(self._ptr)))
+
+    # -- runs in flight ------------------------------------------------------
+
+    def _enter(self) -> None:
+        with self._lock:
+            if self._closed or not self._ptr:
+                raise NemoError(1, "plan was destroyed")
+            self._pending += 1
+
+    def _leave(self) -> None:
+        with self._lock:
+            self._pending -= 1
+            last = self._closed and self._pending == 0
+        if last:
+            self._free()
+
+    def _free(self) -> None:
+        with self._lock:
+            ptr, self._ptr = self._ptr, None
+        if ptr:
+            check(_lib.load().nemo_plan_destroy(ptr))
+
+    # -- EmbeddingPlan -------------------------------------------------------
+
+    def _run_entered(self, ids: np.ndarray, lengths: np.ndarray) -> list[np.ndarray]:
+        try:
+            out = np.empty((self.batch, self.model.hidden), dtype=np.float32)
+            u32p = ctypes.POINTER(ctypes.c_uint32)
+            check(_lib.load().nemo_plan_run(self._ptr, ids.ctypes.data_as(u32p), ids.size,
+                                            lengths.ctypes.data_as(u32p), lengths.size,
+                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+            return [out[i].copy() for i in range(self.batch)]
+        finally:
+            self._leave()
 
     def run_sync(self, ids, lengths) -> list[np.ndarray]:
         """Blocking run: ids [batch * sequence] (padded after each request),
         lengths [batch] -> `batch` float32 [hidden] embeddings."""
-        if self._ptr is None:
-            raise NemoError(1, "plan was destroyed")
         ids, lengths = _u32(ids).reshape(-1), _u32(lengths).reshape(-1)
-        out = np.empty((self.batch, self.model.hidden), dtype=np.float32)
-        u32p = ctypes.POINTER(ctypes.c_uint32)
-        check(_lib.load().nemo_plan_run(self._ptr, ids.ctypes.data_as(u32p), ids.size, lengths.ctypes.data_as(u32p),
-                                        lengths.size, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
-        return [out[i].copy() for i in range(self.batch)]
+        self._enter()
+        return self._run_entered(ids, lengths)
 
-    async def run(self, ids, lengths) -> list[np.ndarray]:
-        """EmbeddingPlan.run (src/webgpu/embedding-engine.ts:8): awaitable;
-        the blocking call runs on a worker thread so distinct plans overlap."""
-        ids, lengths = _u32(ids).copy(), _u32(lengths).copy()
-        return await asyncio.get_running_loop().run_in_executor(None, self.run_sync, ids, lengths)
+    def run(self, ids, lengths) -> "asyncio.Future[list[np.ndarray]]":
+        """EmbeddingPlan.run (src/webgpu/embedding-engine.ts:8): awaitable.
+        The run is counted in flight as this call returns (as the
+        reference's run has written its buffers and submitted by then), and
+        executes on a worker thread so that distinct plans overlap."""
+        ids, lengths = _u32(ids).reshape(-1).copy(), _u32(lengths).reshape(-1).copy()
+        self._enter()
+        try:
+            loop = asyncio.get_running_loop()
+            return loop.run_in_executor(None, self._run_entered, ids, lengths)
+        except BaseException:
+            self._leave()
+            raise
 
     def run_device(self, d_ids: int, lengths, d_out: int, stream: int = 0) -> None:
         """Enqueue on `stream` with ids and output already in device memory."""
         lengths = _u32(lengths).reshape(-1)
-        check(_lib.load().nemo_plan_run_device(self._ptr, ctypes.c_void_p(d_ids),
-                                               lengths.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), lengths.size,
-                                               ctypes.c_void_p(d_out), ctypes.c_void_p(stream or None)))
+        self._enter()
+        try:
+            check(_lib.load().nemo_plan_run_device(self._ptr, ctypes.c_void_p(d_ids),
+                                                   lengths.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                                   lengths.size, ctypes.c_void_p(d_out),
+                                                   ctypes.c_void_p(stream or None)))
+        finally:
+            self._leave()
 
     def profile(self, ids, lengths) -> dict[str, float]:
         """Milliseconds per stage (src/webgpu/model.ts:178-224)."""
@@ -122,8 +174,12 @@ class NemotronHipPlan:
         n = L.nemo_profile_stage_count()
         ms = np.zeros(n, dtype=np.float32)
         u32p = ctypes.POINTER(ctypes.c_uint32)
-        check(L.nemo_plan_profile(self._ptr, ids.ctypes.data_as(u32p), ids.size, lengths.ctypes.data_as(u32p),
-                                  lengths.size, ms.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n))
+        self._enter()
+        try:
+            check(L.nemo_plan_profile(self._ptr, ids.ctypes.data_as(u32p), ids.size, lengths.ctypes.data_as(u32p),
+                                      lengths.size, ms.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n))
+        finally:
+            self._leave()
         return {L.nemo_profile_stage_name(i).decode(): float(ms[i]) for i in range(n)}
 
     def read_buffer(self, name: str) -> np.ndarray:
@@ -131,15 +187,32 @@ class NemotronHipPlan:
         float32 embeddings), as a flat array."""
         L = _lib.load()
         n = ctypes.c_size_t(0)
-        check(L.nemo_plan_read_buffer(self._ptr, name.encode(), None, ctypes.byref(n)))
-        buf = np.empty(n.value, dtype=np.uint8)
-        check(L.nemo_plan_read_buffer(self._ptr, name.encode(), buf.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n)))
+        self._enter()
+        try:
+            check(L.nemo_plan_read_buffer(self._ptr, name.encode(), None, ctypes.byref(n)))
+            buf = np.empty(n.value, dtype=np.uint8)
+            check(L.nemo_plan_read_buffer(self._ptr, name.encode(), buf.ctypes.data_as(ctypes.c_void_p),
+                                          ctypes.byref(n)))
+        finally:
+            self._leave()
         return buf.view(np.float32 if name == "embeddings" else np.float16)
 
     def destroy(self) -> None:
-        if self._ptr:
-            check(_lib.load().nemo_plan_destroy(self._ptr))
-            self._ptr = None
+        """destroy() (src/webgpu/model.ts:141-144): later calls fail with
+        'plan was destroyed'; the device memory is released now, or when
+        the last run in flight settles."""
+        with self._lock:
+            if self._closed:
+                return
+            self._closed = True
+            pending = self._pending
+        if pending == 0:
+            self._free()
+
+    @property
+    def pending(self) -> int:
+        """Runs (and other calls) of the plan in flight."""
+        return self._pending
 
     def __del__(self):
         try:

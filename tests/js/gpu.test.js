@@ -86,6 +86,30 @@ test('distinct plans run concurrently and agree with single runs', async () => {
   singles.forEach((p) => p.destroy());
 });
 
+test('destroy while runs are pending: the runs resolve, the plan is freed after them', async () => {
+  const reqs = golden.requests;
+  const longest = Math.max.apply(null, reqs.map((r) => r.length));
+  const ids = new Uint32Array(reqs.length * longest).fill(11);
+  reqs.forEach((r, i) => ids.set(r, i * longest));
+  const lengths = Uint32Array.from(reqs.map((r) => r.length));
+  const plan = model.createPlan(reqs.length, longest);
+  const first = plan.run(ids, lengths);
+  const second = plan.run(ids, lengths);
+  plan.destroy();
+  await assert.rejects(plan.run(ids, lengths), /plan was destroyed/);
+  const [a, b] = await Promise.all([first, second]);
+  [a, b].forEach((out) => out.forEach((e, i) => assert.ok(cosine(e, expected[i]) >= 0.9999, `request ${i}`)));
+  assert.strictEqual(plan.pending, 0);
+  assert.ok(plan.destroyed);
+  // the addon's own guard: a direct planDestroy with a run in flight also defers
+  const raw = host.native().planCreate(model.handle, reqs.length, longest);
+  const inFlight = host.native().planRun(raw, ids, lengths);
+  host.native().planDestroy(raw);
+  assert.throws(() => host.native().planRun(raw, ids, lengths), /plan was destroyed/);
+  const out = await inFlight;
+  assert.strictEqual(out.length, reqs.length * dims.hidden);
+});
+
 test('synthetic config-dims model: 16 concurrent 150-token requests, one plan run', async () => {
   const cfg = Object.assign(host.configDims(), { layers: 2, mergeAfterLayer: 1 });
   const synth = new host.NemotronHipModel(device, { synthetic: 1003 }, { dims: cfg });

@@ -32,7 +32,7 @@ def test_js_host_on_gpu(tmp_path):
                        text=True, timeout=180)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "4/4 passed" in r.stdout
+    assert "5/5 passed" in r.stdout
 
 
 def test_js_prepack_matches_python(tmp_path):

@@ -25,6 +25,11 @@ def test_js_engine():
     assert "6/6 passed" in _node("engine.test.js")
 
 
+def test_js_plan_lifetime():
+    """destroy() with runs in flight, against a stand-in addon (tests/js/lifecycle.test.js)."""
+    assert "4/4 passed" in _node("lifecycle.test.js")
+
+
 def test_js_host_and_cross_language_pack(tmp_path):
     out = tmp_path / "js.wgpack"
     assert "3/3 passed" in _node("host.test.js", str(out))
