@@ -17,7 +17,17 @@ Printed JSON (one line on stdout):
                per launch / its average launch duration, from HIP events
                bracketing every launch on the plan's stream, against the dense
                fp16 MFMA peak
-  cpu_baseline the oracle's CPU forward of the same encoder (float64 numpy,
+  configs      the other benchmark configurations at their stated shapes:
+               one layer at 150 tokens (N(0, 1) f16 activations), one
+               500-token request, 16 ragged requests, one 5000-token
+               request, each with ms per pass, embeddings/s, tokens/s and
+               the dominant stage's rate against its roofline
+  cpu_baseline the reference's CPU check of the Q4_K dequant-matmul (config
+               1: dequantize each weight row, float64 dot) restated in plain
+               JavaScript, on one thread of the box's Node, with the Node
+               version, the core count and the CPU model
+  cpu_baseline_forward
+               the oracle's CPU forward of the same encoder (float64 numpy,
                binary16 storage) on a bounded sample of the workload
 Progress goes to stderr.
 
@@ -91,7 +101,7 @@ def step_flops(dims) -> float:
     return sum(per_row * (rows_full if l < dims.merge_after_layer else rows_merged) for l in range(dims.layers))
 
 
-def cpu_baseline(model, dims, ids, budget_s: float = 20.0) -> dict:
+def cpu_forward_baseline(model, dims, ids, budget_s: float = 20.0) -> dict:
     """Time the oracle's forward (numpy, float64 BLAS) for whole requests of the
     same workload until about `budget_s` seconds of CPU work are spent."""
     import numpy as np
@@ -122,6 +132,175 @@ def cpu_baseline(model, dims, ids, budget_s: float = 20.0) -> dict:
     return {"value": done / elapsed, "unit": "embeddings/s", "cores": threads, "kind": "port",
             "sample": f"{done} of the 16 requests (150 tokens each) through all {dims.layers} layers, "
                       f"oracle forward (numpy float64, binary16 storage), {elapsed:.1f} s"}
+
+
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def js_cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The reference's CPU check of the Q4_K dequant-matmul (src/main.ts:97-104
+    with dequantizeQ4KBlock, src/gguf/quantization.ts:19-38) for every element
+    of config 1's Y = X W^T (W 2048 x 2048 Q4_K, X 15 x 2048 f16), restated in
+    plain JavaScript (oracle/q4k_matmul_cpu.js) and run on one thread of the
+    box's Node: median milliseconds over as many runs as fit `budget_s`,
+    algorithmic bytes (W + X + f16 Y) per second. The output is checked
+    against the C oracle's restatement, bit for bit."""
+    import shutil
+    import subprocess
+    import tempfile
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    import synth
+    m, n, k = 15, 2048, 2048
+    nbytes = n * k // 256 * 144 + 2 * m * k + 2 * m * n
+    w = synth.random_q4k(1001, n * k // 256)
+    x = synth.normal(1008, m * k).astype(np.float16)
+    node = shutil.which("node")
+    base = {"unit": "GB/s", "cores": 1, "kind": "port", "nproc": os.cpu_count(), "cpu_model": cpu_model_name()}
+    if node is None:
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < budget_s / 3 or reps < 3:
+            oracle.q4k_matmul_cpu(w, x.reshape(m, k), m, n, k)
+            reps += 1
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        return dict(base, value=round(nbytes / (ms * 1e-3) / 1e9, 4), ms_per_call=round(ms, 2), node=None,
+                    sample=f"config 1 by the C restatement (node is not installed): {reps} calls")
+    script = os.path.join(ROOT, "oracle", "q4k_matmul_cpu.js")
+    with tempfile.TemporaryDirectory() as tmp:
+        wp, xp, yp = (os.path.join(tmp, f) for f in ("w.bin", "x.bin", "y.bin"))
+        with open(wp, "wb") as f:
+            f.write(w.tobytes())
+        with open(xp, "wb") as f:
+            f.write(x.tobytes())
+
+        def js(runs, out=None):
+            cmd = [node, script, wp, xp, str(m), str(n), str(k), str(runs)] + ([out] if out else [])
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=600, check=True)
+            return json.loads(r.stdout)
+
+        probe = js(1)
+        runs = int(max(5, min(500, budget_s * 1e3 / max(probe["ms_median"], 1e-3))))
+        res = js(runs, yp)
+        y = np.fromfile(yp, dtype=np.float64).reshape(m, n)
+    want = oracle.q4k_matmul_cpu(w, x.reshape(m, k), m, n, k)
+    ms = res["ms_median"]
+    return dict(base, value=round(nbytes / (ms * 1e-3) / 1e9, 4), ms_per_call=round(ms, 2), node=res["node"],
+                bit_identical_to_c_oracle=bool(np.array_equal(y, want)),
+                sample=f"config 1: Y = X W^T, W 2048 x 2048 Q4_K (seed 1001), X 15 x 2048 f16 (seed 1008); "
+                       f"{runs} runs after one warm-up, median; {nbytes} algorithmic bytes per call")
+
+
+CONFIG4_LENGTHS = [15, 15, 50, 50, 150, 150, 500, 500, 15, 50, 150, 500, 15, 50, 150, 500]
+MATRIX_STAGES = ("qkv", "rope_attention", "attention_output", "ffn_up_gate", "ffn_down")
+
+
+def stage_flops(dims, lengths) -> dict:
+    """Algorithmic flops per pass of the plan's matrix stages (the profile
+    names of src/webgpu/model.ts:198-211): a projection 2 M N K over the layer's
+    packed tokens M (before or after the merge); the attention 4 Hq hd S K
+    per request of S states attending K keys (every third key past the
+    stride threshold)."""
+    from nemo_amd.runtime import contextual_merged_length
+    H, F = dims.hidden, dims.intermediate
+    QW, KW = dims.q_heads * dims.head_dim, dims.kv_heads * dims.head_dim
+    out = dict.fromkeys(MATRIX_STAGES, 0.0)
+    for layer in range(dims.layers):
+        ls = lengths if layer < dims.merge_after_layer else [contextual_merged_length(n) for n in lengths]
+        M = float(sum(ls))
+        out["qkv"] += 2 * M * (QW + 2 * KW) * H
+        out["attention_output"] += 2 * M * H * QW
+        out["ffn_up_gate"] += 2 * M * 2 * F * H
+        out["ffn_down"] += 2 * M * H * F
+        for n in ls:
+            keys = -(-n // dims.kv_stride) if n > dims.kv_stride_threshold else n
+            out["rope_attention"] += 4.0 * QW * n * keys
+    return out
+
+
+def measure_config(torch, stream, plan, ids, lengths, dims, reps: int) -> dict:
+    """One configuration: ms per pass over `reps` passes between HIP events on
+    `stream` (ids and embeddings resident on the device, two passes of
+    warm-up), and the dominant stage of a profiled pass with its rate."""
+    import numpy as np
+    d_ids = torch.from_numpy(np.asarray(ids, np.uint32).view(np.int32).copy()).cuda()
+    d_out = torch.empty((plan.batch, dims.hidden), dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        plan.run_device(d_ids.data_ptr(), lengths, d_out.data_ptr(), stream.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        plan.run_device(d_ids.data_ptr(), lengths, d_out.data_ptr(), stream.cuda_stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    emb = d_out.cpu().numpy()
+    assert np.all(np.abs(np.linalg.norm(emb, axis=1) - 1) < 0.01), "embeddings are not unit vectors"
+    stages = plan.profile(ids, lengths)
+    flops = stage_flops(dims, list(lengths))
+    name = max(stages, key=stages.get)
+    dom = {"stage": name, "ms_per_pass": round(stages[name], 4),
+           "share_of_pass": round(stages[name] / sum(stages.values()), 3)}
+    if name in flops:
+        tf = flops[name] / (stages[name] * 1e-3) / 1e12
+        dom.update({"bound": "mfma", "achieved_tflops": round(tf, 1), "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                    "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "gflop_per_pass": round(flops[name] / 1e9, 2)})
+    total = sum(flops.values())
+    return {"ms_per_pass": round(ms, 4), "passes": reps, "embeddings_per_s": round(plan.batch * 1e3 / ms, 2),
+            "tokens_per_s": round(sum(lengths) * 1e3 / ms, 1), "matrix_tflops": round(total / (ms * 1e-3) / 1e12, 1),
+            "dominant_stage": dom, "stage_ms": {k: round(v, 4) for k, v in stages.items()}}
+
+
+def config_rates(torch, stream, model16, dims) -> dict:
+    """The benchmark configurations besides the headline, each at its own
+    shape on the same 16-layer Q4_K/Q6_K encoder (config 2: a one-layer
+    model of the same dims)."""
+    import numpy as np
+    from nemo_amd import runtime as rt
+    out = {}
+    # config 2: one layer, batch 1, 150 tokens; activations seeded N(0, 1)
+    # f16, fed as 150 embedding rows (token t -> row t)
+    d1 = rt.config_dims()
+    d1.layers, d1.merge_after_layer, d1.vocab = 1, 1, 150
+    table = np.random.default_rng(1002).standard_normal((150, d1.hidden)).astype(np.float16)
+    m1 = rt.NemotronHipModel(None, dims=d1, synthetic_seed=1002, embedding_type=rt.TYPE_F16,
+                             overrides={"token_embd.weight": (rt.TYPE_F16, [d1.hidden, 150], table)})
+    plan = m1.createPlan(1, 150)
+    out["config2_one_layer_150_tokens"] = measure_config(torch, stream, plan, np.arange(150, dtype=np.uint32), [150],
+                                                         d1, 200)
+    plan.destroy()
+    m1.destroy()
+    log(f"config 2: {out['config2_one_layer_150_tokens']['ms_per_pass']} ms per pass")
+
+    def request_ids(seed, lengths, S):
+        rng = np.random.default_rng(seed)
+        ids = np.full(len(lengths) * S, 11, dtype=np.uint32)
+        for b, n in enumerate(lengths):
+            ids[b * S:b * S + n] = rng.integers(1, dims.vocab, size=n)
+            ids[b * S] = 1  # BOS
+        return ids
+
+    for key, seed, lengths, reps in (("config3_500_tokens", 1003, [500], 40),
+                                     ("config4_16_ragged_requests", 1004, CONFIG4_LENGTHS, 20),
+                                     ("config5_5000_tokens", 1005, [5000], 20)):
+        S = max(lengths)
+        plan = model16.createPlan(len(lengths), S)
+        out[key] = measure_config(torch, stream, plan, request_ids(seed, lengths, S), lengths, dims, reps)
+        out[key]["lengths"] = lengths if len(lengths) > 1 else lengths[0]
+        plan.destroy()
+        log(f"{key}: {out[key]['ms_per_pass']} ms per pass, dominant {out[key]['dominant_stage']['stage']}")
+    return out
 
 
 def committed_traffic():
@@ -340,6 +519,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the GEMV / dequant measurements")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other benchmark configurations")
     ap.add_argument("--matrix", action="store_true", help="run the published comparison matrix instead")
     ap.add_argument("--tokens", type=int, default=0, help="--matrix: one row (15, 50, 150, 500, 1500 or 5000)")
     ap.add_argument("--matrix-weights", choices=("q4_0", "q4_k"), default="q4_0")
@@ -433,8 +613,15 @@ def main() -> int:
     result["q4k_gemm_mfma_util_pct"] = round(100 * achieved / MFMA_F16_PEAK_TFLOPS, 1)
     if not args.no_kernels:
         result["kernels"] = kernel_rates(torch, stream)
+    if not args.no_configs:
+        result["configs"] = config_rates(torch, stream, model, dims)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, dims, ids)
+        result["cpu_baseline"] = js_cpu_baseline()
+        gemv = result.get("kernels", {}).get("q4k_gemv_15x2048x2048")
+        if gemv:
+            result["cpu_baseline"]["gpu_gemv_speedup"] = round(gemv["gbs"] / result["cpu_baseline"]["value"], 1)
+        log(f"cpu baseline (JavaScript, 1 thread): {result['cpu_baseline']['ms_per_call']} ms per config-1 call")
+        result["cpu_baseline_forward"] = cpu_forward_baseline(model, dims, ids)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -227,7 +227,8 @@ class NemotronHipModel:
     ``source`` is a ``PrepackedModel`` (src/prepacked/format.ts:54-59), a
     parsed ``GGUFModel`` (src/gguf/types.ts:37-44; dims default to its
     metadata), a mapping name -> (ggml_type, dims, bytes), or None together
-    with ``synthetic_seed`` for seeded synthetic weights.
+    with ``synthetic_seed`` for seeded synthetic weights (``overrides``, a
+    mapping of the same form, then replaces some of them).
     """
 
     # No per-binding storage limit on HIP: the engine's storage cap does not
@@ -235,7 +236,7 @@ class NemotronHipModel:
     maxStorageBufferBindingSize = None
 
     def __init__(self, source=None, dims: Dims | None = None, device: int = 0, synthetic_seed: int | None = None,
-                 embedding_type: int = TYPE_F16):
+                 embedding_type: int = TYPE_F16, overrides: dict | None = None):
         self.ctx = HipContext.shared(device)
         is_gguf = hasattr(source, "dataOffset") and hasattr(source, "metadata") and hasattr(source, "version")
         if dims is None and is_gguf:
@@ -250,6 +251,9 @@ class NemotronHipModel:
             if synthetic_seed is None:
                 raise ValueError("either a source or synthetic_seed is required")
             check(L.nemo_model_synthesize(self._ptr, int(synthetic_seed), int(embedding_type)))
+            # tensors given alongside replace their synthetic counterparts
+            for name, (ggml_type, dims_, data) in (overrides or {}).items():
+                self.set_tensor(name, ggml_type, dims_, data)
         elif hasattr(source, "header") and hasattr(source, "tensors"):
             self._load_prepacked(source)
         elif is_gguf:
