@@ -192,6 +192,25 @@ nemo_status nemo_weight_destroy(nemo_weight* weight);
 nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y, int32_t algo,
                                void* stream);
 
+/* Bytes of the per-GPU static scratch that nemo_weight_matmul_static uses
+ * (64 MiB): split-K partial sums need splits * m * n * 4 bytes, the two-pass
+ * expansion n * k * 2 (a 16384 x 2048 or 2048 x 8192 matrix at most). */
+#define NEMO_STATIC_SCRATCH_BYTES 67108864
+
+/* No counterpart in the reference. nemo_weight_matmul for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc): same algorithms, kernels and
+ * bits, but any scratch (the GEMV's and the split-K tiles' fp32 partial
+ * sums, the two-pass f16 expansion of W) lives in a static array of
+ * NEMO_STATIC_SCRATCH_BYTES that the library holds on each GPU until the
+ * process ends; the call allocates and frees nothing. A call whose scratch
+ * would exceed that size fails with NEMO_ERR_INVALID before launching
+ * anything. Every call on one GPU shares the array: calls that overlap on
+ * one GPU (concurrent streams, or host threads) race and must be ordered by
+ * the caller. */
+nemo_status nemo_weight_matmul_static(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y,
+                                      int32_t algo, void* stream);
+
 /* Decode the uploaded matrix to float32 [n, k] (device pointer); bit-exact
  * with dequantizeQ4KBlock / dequantizeQ6KBlock (src/gguf/quantization.ts:19-74). */
 nemo_status nemo_weight_dequantize(nemo_weight* weight, float* d_out, void* stream);

@@ -241,7 +241,31 @@ constexpr int kNumStages = 11;
 
 struct nemo_ctx {
   int device = 0;
+  void* scratch = nullptr;  // this device's copy of `scratch` (device address)
 };
+
+// Device memory of nemo_weight_matmul_static: the split-K partial sums or the
+// f16 expansion of one weight. Every GPU the library runs on holds its own
+// copy until the process ends, and every call on that GPU shares it. On the
+// host the name is only a stand-in for the symbol, never a device address:
+// device_scratch() looks up each device's copy once, and calls pass that
+// address to the kernels.
+static __device__ __align__(256) unsigned char scratch[NEMO_STATIC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch;  // device -> address of its `scratch`
+
+// The address of `scratch` on `device`, which must be the current device.
+static void* device_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  const auto it = g_scratch.find(device);
+  if (it != g_scratch.end()) return it->second;
+  void* ptr = nullptr;
+  hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  if (!ptr) fail(NEMO_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned a null address");
+  g_scratch[device] = ptr;
+  return ptr;
+}
 
 struct LayerWeights {
   QWeight qkv, o, gate_up, down;
@@ -366,8 +390,10 @@ nemo_status nemo_init(int32_t device, nemo_ctx** out) {
     if (device < 0 || device >= count)
       fail(NEMO_ERR_INVALID, "device " + std::to_string(device) + " out of range (" + std::to_string(count) + ")");
     hip_check(hipSetDevice(device), "hipSetDevice");
+    void* dev_scratch = device_scratch(device);
     auto* c = new nemo_ctx;
     c->device = device;
+    c->scratch = dev_scratch;
     *out = c;
   });
 }
@@ -1126,45 +1152,99 @@ nemo_status nemo_weight_destroy(nemo_weight* weight) {
   });
 }
 
+// The kernels nemo_weight_matmul runs for (w, m, algo), and the scratch they
+// need: fp32 partial sums (GEMV with K split, split-K 64-row tiles) or the
+// f16 expansion of W (two-pass).
+enum MatmulKind { kMmGemv, kMmMid, kMmSplit, kMmTwoPass, kMmFused };
+struct MatmulChoice {
+  MatmulKind kind;
+  int splits;
+  size_t scratch_bytes;
+};
+
+static MatmulChoice choose_matmul(const QWeight& w, int m, int algo) {
+  if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
+  if (algo < 0 || algo > 5) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
+  const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= kGemvMaxM);
+  if (gemv) {
+    if (m > kGemvMaxM) fail(NEMO_ERR_INVALID, "GEMV takes m <= " + std::to_string(kGemvMaxM));
+    return {kMmGemv, gemv_splits(w), gemv_partials_floats(w, m) * 4};
+  }
+  if (algo == NEMO_MATMUL_GEMM_MID) return {kMmMid, 1, 0};
+  if (algo == NEMO_MATMUL_GEMM_SPLIT) {
+    const int sp = mid_splits(w);
+    return sp == 1 ? MatmulChoice{kMmMid, 1, 0} : MatmulChoice{kMmSplit, sp, (size_t)sp * m * w.n * 4};
+  }
+  if (algo == NEMO_MATMUL_TWO_PASS || (algo == NEMO_MATMUL_AUTO && gemm_two_pass(w, m, 1)))
+    return {kMmTwoPass, 1, (size_t)w.n * w.k * 2};
+  return {kMmFused, 1, 0};
+}
+
+// Launch `c` on stream s; `scratch` holds at least c.scratch_bytes.
+static void run_matmul(const MatmulChoice& c, const QWeight& w, const uint16_t* d_x, int m, uint16_t* d_y,
+                       void* scratch, hipStream_t s) {
+  switch (c.kind) {
+    case kMmGemv:
+      hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)scratch, s), "gemv");
+      break;
+    case kMmMid:
+      hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
+      break;
+    case kMmSplit:
+      hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiPartial, c.splits, scratch, w.n, s), "gemm");
+      hip_check(launch_reduce_partials((float*)scratch, c.splits, m, w.n, d_y, w.n, s), "reduce");
+      break;
+    case kMmTwoPass:
+      hip_check(launch_gemm_two_pass(d_x, w.k, w, m, d_y, w.n, (uint16_t*)scratch, s), "two-pass gemm");
+      break;
+    case kMmFused:
+      hip_check(launch_gemm(d_x, w.k, w, d_y, w.n, m, s), "gemm");
+      break;
+  }
+}
+
 nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y, int32_t algo,
                                void* stream) {
   return guarded([&] {
     if (!weight || !d_x || !d_y) fail(NEMO_ERR_INVALID, "null argument");
-    if (m < 1) fail(NEMO_ERR_INVALID, "m must be positive");
+    const QWeight& w = weight->w;
+    const MatmulChoice c = choose_matmul(w, m, algo);
     set_device(weight->ctx);
     hipStream_t s = (hipStream_t)stream;
-    if (algo < 0 || algo > 5) fail(NEMO_ERR_INVALID, "unknown matmul algorithm");
-    const QWeight& w = weight->w;
-    const bool gemv = algo == NEMO_MATMUL_GEMV || (algo == NEMO_MATMUL_AUTO && m <= kGemvMaxM);
-    const bool two_pass =
-        algo == NEMO_MATMUL_TWO_PASS || (algo == NEMO_MATMUL_AUTO && !gemv && gemm_two_pass(w, m, 1));
-    if (gemv) {
-      if (m > kGemvMaxM) fail(NEMO_ERR_INVALID, "GEMV takes m <= " + std::to_string(kGemvMaxM));
-      hip_check(launch_gemv(d_x, w.k, w, d_y, w.n, m, (float*)weight->partials.get(), s), "gemv");
-    } else if (algo == NEMO_MATMUL_GEMM_MID) {
-      hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
-    } else if (algo == NEMO_MATMUL_GEMM_SPLIT) {
-      const int sp = mid_splits(w);
-      if (sp == 1) {
-        hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiStore, 1, d_y, w.n, s), "gemm");
-      } else {
-        const size_t need = (size_t)sp * m * w.n;
-        if (need > weight->split_floats) {
-          if (s) hip_check(hipStreamSynchronize(s), "sync");
-          weight->split_partials.reset();
-          weight->split_partials = dev_alloc(need * 4, "split-K partial sums");
-          weight->split_floats = need;
-        }
-        float* part = (float*)weight->split_partials.get();
-        hip_check(launch_gemm_mid(d_x, w.k, w, m, kEpiPartial, sp, part, w.n, s), "gemm");
-        hip_check(launch_reduce_partials(part, sp, m, w.n, d_y, w.n, s), "reduce");
+    void* scratch_buf = nullptr;
+    if (c.kind == kMmGemv) {
+      scratch_buf = weight->partials.get();  // sized for kGemvMaxM rows at create
+    } else if (c.kind == kMmSplit) {
+      const size_t need = c.scratch_bytes / 4;
+      if (need > weight->split_floats) {
+        if (s) hip_check(hipStreamSynchronize(s), "sync");
+        weight->split_partials.reset();
+        weight->split_partials = dev_alloc(need * 4, "split-K partial sums");
+        weight->split_floats = need;
       }
-    } else if (two_pass) {
-      if (!weight->wexp) weight->wexp = dev_alloc((size_t)w.n * w.k * 2, "f16 weight expansion");
-      hip_check(launch_gemm_two_pass(d_x, w.k, w, m, d_y, w.n, (uint16_t*)weight->wexp.get(), s), "two-pass gemm");
-    } else {
-      hip_check(launch_gemm(d_x, w.k, w, d_y, w.n, m, s), "gemm");
+      scratch_buf = weight->split_partials.get();
+    } else if (c.kind == kMmTwoPass) {
+      if (!weight->wexp) weight->wexp = dev_alloc(c.scratch_bytes, "f16 weight expansion");
+      scratch_buf = weight->wexp.get();
     }
+    run_matmul(c, w, d_x, m, d_y, scratch_buf, s);
+  });
+}
+
+nemo_status nemo_weight_matmul_static(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y,
+                                      int32_t algo, void* stream) {
+  return guarded([&] {
+    if (!weight || !d_x || !d_y) fail(NEMO_ERR_INVALID, "null argument");
+    const QWeight& w = weight->w;
+    const MatmulChoice c = choose_matmul(w, m, algo);
+    if (c.scratch_bytes > (size_t)NEMO_STATIC_SCRATCH_BYTES)
+      fail(NEMO_ERR_INVALID, "this matmul needs " + std::to_string(c.scratch_bytes) +
+                                 " bytes of scratch; the static scratch holds " +
+                                 std::to_string((size_t)NEMO_STATIC_SCRATCH_BYTES));
+    set_device(weight->ctx);
+    // Every kernel writes each scratch element it later reads (one slot per
+    // K split, or the whole expansion), so nothing needs clearing first.
+    run_matmul(c, w, d_x, m, d_y, weight->ctx->scratch, (hipStream_t)stream);
   });
 }
 

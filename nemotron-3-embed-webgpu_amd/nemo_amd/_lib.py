@@ -17,6 +17,7 @@ STATUS_NAMES = {1: "invalid", 2: "missing", 3: "device", 4: "out of memory", 5: 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 12, 14
 TYPE_Q4_0_TILE32 = 258  # wgpack q4_0-tile32-compact records (include/nemo.h)
 MATMUL_AUTO, MATMUL_GEMM, MATMUL_GEMV, MATMUL_TWO_PASS, MATMUL_GEMM_MID, MATMUL_GEMM_SPLIT = 0, 1, 2, 3, 4, 5
+STATIC_SCRATCH_BYTES = 64 << 20  # NEMO_STATIC_SCRATCH_BYTES
 
 # Every symbol include/nemo.h declares.
 EXPORTED = [
@@ -25,7 +26,8 @@ EXPORTED = [
     "nemo_model_get_tensor", "nemo_model_destroy", "nemo_plan_create", "nemo_plan_run", "nemo_plan_run_device",
     "nemo_plan_profile", "nemo_profile_stage_count", "nemo_profile_stage_name", "nemo_plan_destroy",
     "nemo_plan_shape", "nemo_plan_read_buffer",
-    "nemo_weight_create", "nemo_weight_destroy", "nemo_weight_matmul", "nemo_weight_dequantize", "nemo_dequantize",
+    "nemo_weight_create", "nemo_weight_destroy", "nemo_weight_matmul", "nemo_weight_matmul_static",
+    "nemo_weight_dequantize", "nemo_dequantize",
     "nemo_requantize_q40",
 ]
 
@@ -88,6 +90,7 @@ def load() -> ctypes.CDLL:
         "nemo_weight_create": (i32, [vp, i32, i32, i32, vp, sz, pp]),
         "nemo_weight_destroy": (i32, [vp]),
         "nemo_weight_matmul": (i32, [vp, vp, i32, vp, i32, vp]),
+        "nemo_weight_matmul_static": (i32, [vp, vp, i32, vp, i32, vp]),
         "nemo_weight_dequantize": (i32, [vp, vp, vp]),
         "nemo_dequantize": (i32, [i32, vp, ctypes.c_int64, vp, vp, vp]),
         "nemo_requantize_q40": (i32, [vp, i32, vp, sz, ctypes.c_int64, ctypes.c_int64, vp, sz]),

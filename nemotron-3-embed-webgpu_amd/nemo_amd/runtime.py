@@ -328,6 +328,12 @@ class QuantWeight:
         check(_lib.load().nemo_weight_matmul(self._ptr, ctypes.c_void_p(d_x), m, ctypes.c_void_p(d_y), algo,
                                              ctypes.c_void_p(stream or None)))
 
+    def matmul_static(self, d_x: int, m: int, d_y: int, algo: int = _lib.MATMUL_AUTO, stream: int = 0) -> None:
+        """matmul() without allocating: scratch in the library's per-GPU static
+        array (nemo_weight_matmul_static; calls on one GPU must not overlap)."""
+        check(_lib.load().nemo_weight_matmul_static(self._ptr, ctypes.c_void_p(d_x), m, ctypes.c_void_p(d_y), algo,
+                                                    ctypes.c_void_p(stream or None)))
+
     def dequantize(self, d_out: int, stream: int = 0) -> None:
         check(_lib.load().nemo_weight_dequantize(self._ptr, ctypes.c_void_p(d_out), ctypes.c_void_p(stream or None)))
 

@@ -53,6 +53,7 @@ def test_constants_match_header():
         oracle.GGML_Q4_0, oracle.GGML_Q4_K, oracle.GGML_Q6_K)
     assert (d["NEMO_MATMUL_AUTO"], d["NEMO_MATMUL_GEMM"], d["NEMO_MATMUL_GEMV"], d["NEMO_MATMUL_TWO_PASS"]) == (
         _lib.MATMUL_AUTO, _lib.MATMUL_GEMM, _lib.MATMUL_GEMV, _lib.MATMUL_TWO_PASS)
+    assert d["NEMO_STATIC_SCRATCH_BYTES"] == _lib.STATIC_SCRATCH_BYTES == 64 << 20
 
 
 def test_host_only_calls():
