@@ -17,7 +17,12 @@ Printed JSON (one line on stdout):
                per launch / its average launch duration, from HIP events
                bracketing every launch on the plan's stream, against the dense
                fp16 MFMA peak
-  configs      the other benchmark configurations at their stated shapes:
+  q4k_gemm_mfma_util
+               that flop rate as % of the peak, next to the MFMA pipes' busy
+               share of the same GEMM launches from hardware counters
+               (SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE, read from the
+               committed rocprofv3 summary)
+  configs     the other benchmark configurations at their stated shapes:
                one layer at 150 tokens (N(0, 1) f16 activations), one
                500-token request, 16 ragged requests, one 5000-token
                request, each with ms per pass, embeddings/s, tokens/s and
@@ -317,6 +322,35 @@ def committed_traffic():
     return None
 
 
+def committed_mfma_busy():
+    """MFMA busy share of the gate/up GEMM launches from the committed
+    rocprofv3 counter summary (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE
+    per launch), averaged over the launches weighted by their durations, or
+    None."""
+    path = os.path.join(ROOT, "profiles", "gemm_projections_16x150.md")
+    try:
+        with open(path) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    header = next((ln for ln in lines if ln.startswith("| projection |")), None)
+    if header is None:
+        return None
+    cols = [c.strip() for c in header.strip("|").split("|")]
+    try:
+        i_calls, i_us, i_busy = cols.index("calls"), cols.index("avg us"), cols.index("MFMA busy %")
+    except ValueError:
+        return None
+    num = den = 0.0
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        if len(cells) == len(cols) and cells[0].startswith("gate/up"):
+            t = float(cells[i_calls]) * float(cells[i_us])
+            num += t * float(cells[i_busy])
+            den += t
+    return round(num / den, 1) if den else None
+
+
 def _time_calls(torch, stream, fn, calls: int) -> tuple[float, str]:
     """Average microseconds per call of `fn(i)` over `calls` back-to-back
     calls, between HIP events on `stream`. The calls are captured once into a
@@ -610,7 +644,15 @@ def main() -> int:
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "traffic_source": "profiles/gate_up_traffic_16x150.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)"},
     }
+    # The metric's "MFMA util %": algorithmic flop rate of the gate/up launch
+    # against the dense peak (measured here), and the MFMA pipes' busy share
+    # of the same GEMM launches from hardware counters (committed profile).
     result["q4k_gemm_mfma_util_pct"] = round(100 * achieved / MFMA_F16_PEAK_TFLOPS, 1)
+    result["q4k_gemm_mfma_util"] = {
+        "flop_rate_pct_of_peak": result["q4k_gemm_mfma_util_pct"],
+        "mfma_busy_pct_counters": committed_mfma_busy(),
+        "busy_source": "profiles/gemm_projections_16x150.md (rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE, "
+                       "gate/up GEMM launches weighted by duration)"}
     if not args.no_kernels:
         result["kernels"] = kernel_rates(torch, stream)
     if not args.no_configs:
