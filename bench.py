@@ -25,7 +25,8 @@ Printed JSON (one line on stdout):
   configs     the other benchmark configurations at their stated shapes:
                one layer at 150 tokens (N(0, 1) f16 activations), one
                500-token request, 16 ragged requests, one 5000-token
-               request, each with ms per pass, embeddings/s, tokens/s and
+               request (also under README.md:26's rule: every key before
+               the merge), each with ms per pass, embeddings/s, tokens/s and
                the dominant stage's rate against its roofline
   cpu_baseline the reference's CPU check of the Q4_K dequant-matmul (config
                1: dequantize each weight row, float64 dot) restated in plain
@@ -227,8 +228,9 @@ def stage_flops(dims, lengths) -> dict:
         out["attention_output"] += 2 * M * H * QW
         out["ffn_up_gate"] += 2 * M * 2 * F * H
         out["ffn_down"] += 2 * M * H * F
+        dense = dims.kv_dense_before_merge and layer < dims.merge_after_layer
         for n in ls:
-            keys = -(-n // dims.kv_stride) if n > dims.kv_stride_threshold else n
+            keys = -(-n // dims.kv_stride) if n > dims.kv_stride_threshold and not dense else n
             out["rope_attention"] += 4.0 * QW * n * keys
     return out
 
@@ -305,6 +307,18 @@ def config_rates(torch, stream, model16, dims) -> dict:
         out[key]["lengths"] = lengths if len(lengths) > 1 else lengths[0]
         plan.destroy()
         log(f"{key}: {out[key]['ms_per_pass']} ms per pass, dominant {out[key]['dominant_stage']['stage']}")
+    # config 5 under the rule README.md:26 states (every key in layers 1-4,
+    # every third key after the merge at 3200 states) on the same weights
+    dd = rt.config_dims()
+    dd.kv_dense_before_merge = 1
+    md = rt.NemotronHipModel(None, dims=dd, synthetic_seed=SEED, embedding_type=rt.TYPE_F16)
+    plan = md.createPlan(1, 5000)
+    key = "config5_5000_tokens_dense_before_merge"
+    out[key] = measure_config(torch, stream, plan, request_ids(1005, [5000], 5000), [5000], dd, 20)
+    out[key]["lengths"] = 5000
+    plan.destroy()
+    md.destroy()
+    log(f"{key}: {out[key]['ms_per_pass']} ms per pass")
     return out
 
 

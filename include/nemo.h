@@ -65,6 +65,10 @@ typedef struct nemo_dims {
   float rope_theta;            /* 1e6: model.ts:28 */
   int32_t kv_stride_threshold; /* 2048: ops.ts:258 */
   int32_t kv_stride;           /* 3: ops.ts:258 */
+  int32_t kv_dense_before_merge; /* 0: the code's rule (ops.ts:258) in every layer, so a request longer
+                                    than the threshold samples keys before the merge too; 1: the rule
+                                    README.md:26 states: layers before the merge attend every key, and
+                                    merged sequences through the threshold use full attention */
 } nemo_dims;
 
 /* Fills the reference model's constants (src/webgpu/model.ts:19-28). */

@@ -358,6 +358,8 @@ static void validate_dims(const nemo_dims& d) {
     fail(NEMO_ERR_INVALID, "merge_after_layer must lie in [0, layers]");
   if (d.vocab <= 0) fail(NEMO_ERR_INVALID, "vocab must be positive");
   if (d.kv_stride < 1) fail(NEMO_ERR_INVALID, "kv_stride must be >= 1");
+  if (d.kv_dense_before_merge != 0 && d.kv_dense_before_merge != 1)
+    fail(NEMO_ERR_INVALID, "kv_dense_before_merge must be 0 or 1");
 }
 
 // Every nemo_* definition below takes C linkage from its declaration in nemo.h.
@@ -376,6 +378,7 @@ void nemo_dims_reference(nemo_dims* out) {
   out->rope_theta = 1e6f;
   out->kv_stride_threshold = 2048;
   out->kv_stride = 3;
+  out->kv_dense_before_merge = 0;
 }
 
 const char* nemo_last_error(void) { return g_last_error.c_str(); }
@@ -980,7 +983,10 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     int longest = 0;
     for (int b = 0; b < rows.count; ++b) longest = std::max(longest, rows.start[b + 1] - rows.start[b]);
     const bool prep = p->attn_ks && longest > attn_round_keys(d.head_dim);
-    hip_check(launch_attention(qkv, QKV, rope, rows, d.q_heads, d.kv_heads, d.head_dim, d.kv_stride_threshold,
+    // Every key before the merge under the README's rule (no request length
+    // exceeds INT32_MAX); the plan's key buffers hold every key of a request.
+    const int stride_threshold = d.kv_dense_before_merge && full ? INT32_MAX : d.kv_stride_threshold;
+    hip_check(launch_attention(qkv, QKV, rope, rows, d.q_heads, d.kv_heads, d.head_dim, stride_threshold,
                                d.kv_stride, attn, s, prep ? (uint16_t*)p->attn_ks.get() : nullptr,
                                prep ? (uint16_t*)p->attn_vts.get() : nullptr, p->attn_keys_cap),
               "attention");

@@ -19,6 +19,9 @@ export interface ModelDims {
   hidden: number; qHeads: number; kvHeads: number; headDim: number; intermediate: number; layers: number;
   vocab: number; mergeAfterLayer: number; rmsEpsilon: number; ropeTheta: number; kvStrideThreshold: number;
   kvStride: number;
+  /** 0: the reference code's stride rule in every layer (src/webgpu/ops.ts:258); 1: README.md:26's rule,
+   *  every key before the merge. */
+  kvDenseBeforeMerge: number;
 }
 
 export declare const GGMLType: { readonly F32: 0; readonly F16: 1; readonly Q4_0: 2; readonly Q4_K: 12; readonly Q6_K: 14 };

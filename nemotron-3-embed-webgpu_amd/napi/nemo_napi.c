@@ -160,7 +160,7 @@ static napi_value js_version(napi_env env, napi_callback_info info) {
 
 static const char* kDimNames[] = {"hidden", "qHeads", "kvHeads", "headDim", "intermediate", "layers",
                                   "vocab", "mergeAfterLayer", "rmsEpsilon", "ropeTheta", "kvStrideThreshold",
-                                  "kvStride"};
+                                  "kvStride", "kvDenseBeforeMerge"};
 
 static napi_value dims_to_js(napi_env env, const nemo_dims* d) {
   napi_value o, v;
@@ -179,6 +179,8 @@ static napi_value dims_to_js(napi_env env, const nemo_dims* d) {
   CHECK_NAPI(env, napi_set_named_property(env, o, kDimNames[10], v));
   CHECK_NAPI(env, napi_create_int32(env, d->kv_stride, &v));
   CHECK_NAPI(env, napi_set_named_property(env, o, kDimNames[11], v));
+  CHECK_NAPI(env, napi_create_int32(env, d->kv_dense_before_merge, &v));
+  CHECK_NAPI(env, napi_set_named_property(env, o, kDimNames[12], v));
   return o;
 }
 
@@ -188,7 +190,7 @@ static int dims_from_js(napi_env env, napi_value o, nemo_dims* d) {
                    &d->vocab, &d->merge_after_layer};
   napi_value v;
   double x;
-  for (int i = 0; i < 12; ++i) {
+  for (int i = 0; i < 13; ++i) {
     if (napi_get_named_property(env, o, kDimNames[i], &v) != napi_ok || napi_get_value_double(env, v, &x) != napi_ok) {
       char msg[80];
       snprintf(msg, sizeof msg, "dims.%s must be a number", kDimNames[i]);
@@ -199,7 +201,8 @@ static int dims_from_js(napi_env env, napi_value o, nemo_dims* d) {
     else if (i == 8) d->rms_epsilon = (float)x;
     else if (i == 9) d->rope_theta = (float)x;
     else if (i == 10) d->kv_stride_threshold = (int32_t)x;
-    else d->kv_stride = (int32_t)x;
+    else if (i == 11) d->kv_stride = (int32_t)x;
+    else d->kv_dense_before_merge = (int32_t)x;
   }
   return 1;
 }

@@ -47,6 +47,7 @@ class Dims(ctypes.Structure):
         ("head_dim", ctypes.c_int32), ("intermediate", ctypes.c_int32), ("layers", ctypes.c_int32),
         ("vocab", ctypes.c_int32), ("merge_after_layer", ctypes.c_int32), ("rms_epsilon", ctypes.c_float),
         ("rope_theta", ctypes.c_float), ("kv_stride_threshold", ctypes.c_int32), ("kv_stride", ctypes.c_int32),
+        ("kv_dense_before_merge", ctypes.c_int32),
     ]
 
 

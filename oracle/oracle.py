@@ -60,8 +60,12 @@ forward / forward_request      graph wiring (src/webgpu/model.ts:113-138,
                                which residual add; a value-passthrough layer
                                after the merge -> the normalized stream is
                                merged as it is; RoPE positions restart after
-                               the merge; each pin fails on a planted wiring
-                               mistake (tests/test_oracle_wiring*.py); batch
+                               the merge; the key set each layer attends
+                               under the code's rule and README.md:26's
+                               (kv_dense_before_merge), by uniform attention
+                               over it; each pin fails on a planted wiring
+                               mistake or the other key set
+                               (tests/test_oracle_wiring*.py); batch
                                composition invariance
 =============================  ==============================================
 """
@@ -233,6 +237,9 @@ class Dims:
     rope_theta: float = 1_000_000.0
     kv_stride_threshold: int = 2048   # src/webgpu/ops.ts:258
     kv_stride: int = 3
+    # 0: the code's rule (src/webgpu/ops.ts:258) in every layer; 1: the rule
+    # README.md:26 states, every key in the layers before the merge.
+    kv_dense_before_merge: int = 0
 
     @property
     def qkv_width(self) -> int:
@@ -422,7 +429,8 @@ def forward_request(model: Model, ids: np.ndarray, trace: dict | None = None) ->
         qkv = matmul(norm, model.qkv[layer])
         q, k = rope(qkv, np.arange(n), table, d)
         v = qkv[:, (Hq + Hkv) * hd:].reshape(n, Hkv, hd)
-        att = attention(q, k, v, d, d.kv_stride_threshold, d.kv_stride).reshape(n, Hq * hd)
+        dense = d.kv_dense_before_merge and layer < d.merge_after_layer
+        att = attention(q, k, v, d, n if dense else d.kv_stride_threshold, d.kv_stride).reshape(n, Hq * hd)
         delta_o = matmul(att, model.attn_output[layer])
         x, norm = rms_norm(x, model.ffn_norm[layer], d.rms_epsilon, delta_o)
         gate_up = matmul(norm, model.gate_up[layer])

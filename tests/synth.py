@@ -215,7 +215,7 @@ def oracle_model(dims, tensors: dict):
                      intermediate=dims.intermediate, layers=dims.layers, vocab=dims.vocab,
                      merge_after_layer=dims.merge_after_layer, rms_epsilon=float(np.float32(dims.rms_epsilon)),
                      rope_theta=float(np.float32(dims.rope_theta)), kv_stride_threshold=dims.kv_stride_threshold,
-                     kv_stride=dims.kv_stride)
+                     kv_stride=dims.kv_stride, kv_dense_before_merge=dims.kv_dense_before_merge)
     vec = lambda name: np.frombuffer(tensors[name][2], np.float32)
     et, _, eb = tensors["token_embd.weight"]
     m = oracle.Model(od, et, np.frombuffer(eb, np.uint8) if et == 14 else np.frombuffer(eb, np.float16),

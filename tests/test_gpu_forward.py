@@ -101,6 +101,36 @@ def test_long_requests_prepared_keys_match_oracle(torch_cuda, hd, Hq, Hkv):
         assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
 
 
+def test_dense_before_merge_rule_matches_oracle(torch_cuda):
+    """README.md:26's key rule (kv_dense_before_merge = 1): requests of 450
+    to 700 tokens attend every key in the layer before the merge (prepared
+    keys, stride 1) and every third key after it once the merged length
+    (288 to 448) exceeds the threshold 400; against the oracle under the
+    same rule, and different from the code's rule on the same weights."""
+    kw = dict(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, layers=3, vocab=300,
+              merge_after_layer=1, kv_stride_threshold=400)
+    lengths = [700, 30, 520, 450]
+    seqs = [[1] + list(synth.randint(1400 + i, n - 1, 2, 300)) for i, n in enumerate(lengths)]
+    ids, lens = _padded(seqs, 700)
+    out = {}
+    for rule in (1, 0):
+        dims = rt.make_dims(kv_dense_before_merge=rule, **kw)
+        tensors = synth.model_tensors(dims, seed=1401, embedding_type=1)
+        model = rt.NemotronHipModel(tensors, dims=dims)
+        plan = model.createPlan(len(seqs), 700)
+        out[rule] = plan.run_sync(ids, lens)
+        plan.destroy()
+        if rule == 1:
+            om = synth.oracle_model(dims, tensors)
+            for i, s in enumerate(seqs):
+                c = _cos(out[1][i], oracle.forward_request(om, np.array(s)))
+                assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
+        model.destroy()
+    for i, n in enumerate(lengths):
+        same = np.array_equal(out[0][i].view(np.uint32), out[1][i].view(np.uint32))
+        assert same == (n <= 400), f"request {i} (len {n})"
+
+
 def test_request_past_16384_tokens_matches_oracle(torch_cuda):
     """17,000 tokens: queries at positions >= 16384 scale their scores by the
     temperature 1 + 0.1 ln(floor(i / 16384) + 1) (src/webgpu/ops.ts:241),

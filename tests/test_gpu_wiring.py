@@ -62,8 +62,8 @@ def tensors_for(model):
     return t
 
 
-def run(model_tensors, requests):
-    model = rt.NemotronHipModel(model_tensors, dims=dims())
+def run(model_tensors, requests, model_dims=None):
+    model = rt.NemotronHipModel(model_tensors, dims=model_dims or dims())
     S = max(len(r) for r in requests)
     ids = np.full(len(requests) * S, 11, dtype=np.uint32)
     for i, r in enumerate(requests):
@@ -136,3 +136,31 @@ def test_fused_rope_uses_merged_positions(torch_cuda):
     err_bad = np.linalg.norm(a - bad) / np.linalg.norm(bad)
     assert err <= 1e-2, f"attention relative error {err}"
     assert err_bad > 0.05 and err_bad > 20 * err, (err, err_bad)
+
+
+@pytest.mark.parametrize("dense_before_merge", [0, 1])
+def test_key_sampling_rule_before_and_after_the_merge(torch_cuda, dense_before_merge):
+    """The attention's key set per layer under both rules (threshold 4, a
+    7-token request, 5 states after the merge): uniform attention over the
+    keys a layer attends makes the embedding a closed form of that key set
+    (tests/test_oracle_wiring.py). The code's rule (src/webgpu/ops.ts:258)
+    attends keys 0, 3, 6 before the merge; README.md:26's attends all 7;
+    both attend 0, 3 after it."""
+    from dataclasses import replace
+    d = replace(D, kv_stride_threshold=4, kv_dense_before_merge=dense_before_merge)
+    rd = dims()
+    rd.kv_stride_threshold, rd.kv_dense_before_merge = 4, dense_before_merge
+    emb = W.embedding_table()
+    norms = W.random_norms(120, D.layers)
+    w_out = (1.0 + 0.4 * synth.normal(121, H)).astype(np.float32)
+    ids = [2, 7, 11, 19, 23, 29, 31]
+    for layer, keys, other in ((0, range(7) if dense_before_merge else [0, 3, 6],
+                                [0, 3, 6] if dense_before_merge else range(7)),
+                               (4, [0, 3], range(5))):
+        m = W.uniform_passthrough_model(emb, norms, w_out, layer, d)
+        got, _ = run(tensors_for(m), [ids], rd)
+        want = W.uniform_closed_form(emb, ids, norms, w_out, layer, list(keys))
+        mutant = W.uniform_closed_form(emb, ids, norms, w_out, layer, list(other))
+        c = W.cos(got[0], want)
+        assert c >= 0.99999, f"layer {layer}: cosine {c}"
+        assert W.cos(got[0], mutant) < c - 1e-5, f"layer {layer}"

@@ -239,3 +239,68 @@ def test_rope_positions_restart_in_the_merged_sequence():
             qb, kb = oracle.rope(raw, pos_bad, table, D)
             bad = oracle.attention(qb, kb, v, D).reshape(n, -1)
             assert np.abs(bad.astype(np.float64) - att.astype(np.float64)).max() > 1e-3
+
+
+# --------------------------------------------------------------------------
+# which keys each layer attends: the code's rule and README.md:26's
+# --------------------------------------------------------------------------
+
+def uniform_passthrough_model(emb, norms, w_out, layer, dims=D):
+    """Layer `layer` with Wq = Wk = 0 (every score 0, so the attention
+    weights are uniform over the keys it attends), Wv selecting hidden
+    columns 0..Hkv*hd-1 and O the identity; every other projection zero."""
+    qkv = [np.zeros((QKV, H), np.float32) for _ in range(dims.layers)]
+    o = [np.zeros((H, dims.q_heads * dims.head_dim), np.float32) for _ in range(dims.layers)]
+    kv_cols = dims.kv_heads * dims.head_dim
+    v0 = (dims.q_heads + dims.kv_heads) * dims.head_dim
+    qkv[layer][v0 + np.arange(kv_cols), np.arange(kv_cols)] = 1.0
+    o[layer][:] = np.eye(H, dtype=np.float32)
+    m = make_model(emb, norms, random_norms(90, dims.layers), w_out, qkv=qkv, o=o)
+    m.dims = dims
+    return m
+
+
+def uniform_closed_form(emb, ids, norms, w_out, layer, keys):
+    """The embedding of `uniform_passthrough_model` when the pass-through
+    layer attends key positions `keys` of its sequence: that layer adds,
+    for every query, the mean over those keys of its input's normalized
+    rows' first Hkv*hd columns (per KV head); layers before the merge see
+    the token rows, layers after it the merged rows."""
+    S = len(ids)
+    x = emb[np.array(ids)]
+    if layer >= D.merge_after_layer:
+        x = merged(x, S)
+        nm = merged(rms_rows(emb[np.array(ids)], norms[layer]), S)
+    else:
+        nm = rms_rows(x, norms[layer])
+    v = nm[np.array(keys), :D.kv_heads * D.head_dim].astype(np.float64)
+    per_kv = [f16(v[:, g * D.head_dim:(g + 1) * D.head_dim].mean(axis=0)) for g in range(D.kv_heads)]
+    att = np.concatenate([per_kv[h // (D.q_heads // D.kv_heads)] for h in range(D.q_heads)]).astype(np.float64)
+    x = f16(x.astype(np.float64) + att[None, :])
+    if layer < D.merge_after_layer:
+        x = merged(x, S)
+    return l2(rms_rows(x, w_out).astype(np.float64).mean(axis=0))
+
+
+@pytest.mark.parametrize("dense_before_merge", [0, 1])
+def test_key_sampling_rule_before_and_after_the_merge(dense_before_merge):
+    """With threshold 4, a 7-token request (5 states after the merge) is
+    longer than the threshold in every layer. The code's rule (ops.ts:258,
+    kv_dense_before_merge 0) attends keys 0, 3, 6 in the first four layers
+    and 0, 3 after the merge; README.md:26's rule (1) attends all 7 keys
+    before the merge and the same 0, 3 after it."""
+    from dataclasses import replace
+    d = replace(D, kv_stride_threshold=4, kv_dense_before_merge=dense_before_merge)
+    emb = embedding_table()
+    norms = random_norms(120, D.layers)
+    w_out = (1.0 + 0.4 * synth.normal(121, H)).astype(np.float32)
+    ids = [2, 7, 11, 19, 23, 29, 31]
+    for layer, keys, other in ((0, range(7) if dense_before_merge else [0, 3, 6],
+                                [0, 3, 6] if dense_before_merge else range(7)),
+                               (4, [0, 3], range(5))):
+        m = uniform_passthrough_model(emb, norms, w_out, layer, d)
+        want = uniform_closed_form(emb, ids, norms, w_out, layer, list(keys))
+        got = oracle.forward_request(m, np.array(ids))
+        assert np.allclose(got, want, atol=1e-7, rtol=0), f"layer {layer}"
+        mutant = uniform_closed_form(emb, ids, norms, w_out, layer, list(other))
+        assert cos(mutant, want) < 1 - 1e-4, f"layer {layer}: the other key set gives the same embedding"
