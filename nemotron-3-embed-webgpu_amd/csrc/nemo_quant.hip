@@ -81,7 +81,7 @@ struct GvQ4K {
     const uint32_t words[4] = {q.x, q.y, q.z, q.w};
     float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bytes4_fma(opaque((words[i] >> sh) & 0x0f0f0f0fu), dsc, ndm, v + 4 * i);
+    for (int i = 0; i < 4; ++i) nibbles4_fma((words[i] >> sh) & 0x0f0f0f0fu, dsc, ndm, v + 4 * i);
     f0 = to_half8(v);
     f1 = to_half8(v + 8);
   }
@@ -168,7 +168,7 @@ struct GvQ40 {
     const uint32_t words[4] = {q.x, q.y, q.z, q.w};
     float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bytes4_fma(opaque((words[i] >> sh) & 0x0f0f0f0fu), d, -8.0f * d, v + 4 * i);
+    for (int i = 0; i < 4; ++i) nibbles4_fma((words[i] >> sh) & 0x0f0f0f0fu, d, -8.0f * d, v + 4 * i);
     f0 = to_half8(v);
     f1 = to_half8(v + 8);
   }
@@ -237,10 +237,12 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
         xa[2 * r] = *(const half8v*)(sx + 512 * c + 16 * ((k >> 3) ^ c));
         xa[2 * r + 1] = *(const half8v*)(sx + 512 * c + 16 * (((k >> 3) + 1) ^ c));
       }
+      // Tile by tile: the weight loads return in issue order, so the first
+      // tile's decode and MFMAs start while the later tiles' bytes arrive.
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int t = 0; t < kGvTiles; ++t)
 #pragma unroll
-        for (int t = 0; t < kGvTiles; ++t) {
+        for (int r = 0; r < 4; ++r) {
           if (g == 0) raw[t].run(kq, r, wf[t][2 * r], wf[t][2 * r + 1]);
           acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r], wf[t][2 * r], acc[g][t], 0, 0, 0);
           acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * r + 1], wf[t][2 * r + 1], acc[g][t], 0, 0, 0);
@@ -568,8 +570,8 @@ __device__ __forceinline__ void q4k_block_part(const uint8_t* __restrict__ blk, 
     const float dsc = high ? dsc1 : dsc0, ndm = high ? ndm1 : ndm0;
     const int sh = 4 * high;
     float v[8];
-    bytes4_fma(opaque((q[i][0] >> sh) & 0x0f0f0f0fu), dsc, ndm, v);
-    bytes4_fma(opaque((q[i][1] >> sh) & 0x0f0f0f0fu), dsc, ndm, v + 4);
+    nibbles4_fma((q[i][0] >> sh) & 0x0f0f0f0fu, dsc, ndm, v);
+    nibbles4_fma((q[i][1] >> sh) & 0x0f0f0f0fu, dsc, ndm, v + 4);
     const int64_t o = o0 + 64 * i + 8 * c;
     if constexpr (NT) {
       if (out32) {
