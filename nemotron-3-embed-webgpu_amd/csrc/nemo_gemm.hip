@@ -491,8 +491,9 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
 // WM waves along M (32 MI rows each) x BN/128 along N (128 columns each).
 // LDS: two stages of the BM x 64 X tile and the BN x 64 W tile (128 bytes
 // per row). Configurations: 256 x 256 (8 waves of 64 x 128), 256 x 128 (4
-// waves of 64 x 128), 192 x 256 (4 waves of 96 x 128), 128 x 256 (8 waves of
-// 32 x 128) and 128 x 128 (4 waves of 32 x 128): the tile grid is chosen per
+// waves of 64 x 128), 192 x 256 (4 waves of 96 x 128), 384 x 256 (8 waves of
+// 96 x 128), 128 x 256 (8 waves of 32 x 128) and 128 x 128 (4 waves of
+// 32 x 128): the tile grid is chosen per
 // problem by counting rounds of 256 workgroups, and every configuration
 // issues the same MFMA sequence per output element.
 constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
@@ -677,8 +678,21 @@ static bool use_mid(const QWeight& w, int m, int splits) {
 // f16 GEMM tile configurations of the two-pass path.
 // kF16T256Tail: 256 x 256 tiles over the rows that fill whole rounds of 256
 // workgroups, then 128 x 256 tiles over the rest in a second launch.
-enum F16Tile { kF16None = 0, kF16T256x256, kF16T256x128, kF16T192x256, kF16T128x256, kF16T256Tail, kF16T128x128 };
-static int f16_bm(int t) { return t == kF16T192x256 ? 192 : (t == kF16T128x256 || t == kF16T128x128) ? 128 : 256; }
+// kF16T384x256: 8 waves of 96 x 128, the whole 160 KB of LDS (two stages of
+// 384 + 256 rows of 128 bytes).
+enum F16Tile {
+  kF16None = 0,
+  kF16T256x256,
+  kF16T256x128,
+  kF16T192x256,
+  kF16T128x256,
+  kF16T256Tail,
+  kF16T128x128,
+  kF16T384x256
+};
+static int f16_bm(int t) {
+  return t == kF16T384x256 ? 384 : t == kF16T192x256 ? 192 : (t == kF16T128x256 || t == kF16T128x128) ? 128 : 256;
+}
 static int f16_bn(int t) { return (t == kF16T256x128 || t == kF16T128x128) ? 128 : 256; }
 
 // Rows of a kF16T256Tail launch's 256 x 256 part (n % 256 == 0).
@@ -707,6 +721,12 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     const int t256 = mt * (w.n / 256) * splits, t192 = ((m + 191) / 192) * (w.n / 256) * splits;
     int best = kF16T256x256, cost = 1000 * ((t256 + 255) / 256);
     if (904 * ((t192 + 255) / 256) < cost) best = kF16T192x256, cost = 904 * ((t192 + 255) / 256);
+    // 384-row tiles (a round measured at 1.525 times a 256-row round: 1.5 times
+    // the work, less LDS traffic per MFMA) when they need fewer rounds: 1536
+    // tokens of the gate/up projection fill exactly one round of them
+    // (104.6 us for the f16 GEMM against 127.5 on the tiling below).
+    const int t384 = ((m + 383) / 384) * (w.n / 256) * splits;
+    if (1525 * ((t384 + 255) / 256) < cost) best = kF16T384x256, cost = 1525 * ((t384 + 255) / 256);
     // Whole rounds of 256-row tiles, then the rows left on 128-row tiles in
     // a second launch, a round of those charged 0.65 of a 256-row round.
     // With that charge the encoder's shapes pick the faster tiling (gate/up,
@@ -809,6 +829,7 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
     case kF16T192x256: launch_f16<256, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T128x256: launch_f16<256, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T128x128: launch_f16<128, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T384x256: launch_f16<256, 4, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
