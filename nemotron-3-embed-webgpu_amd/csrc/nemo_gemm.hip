@@ -492,8 +492,8 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
 // LDS: two stages of the BM x 64 X tile and the BN x 64 W tile (128 bytes
 // per row). Configurations: 256 x 256 (8 waves of 64 x 128), 256 x 128 (4
 // waves of 64 x 128), 192 x 256 (4 waves of 96 x 128), 384 x 256 (8 waves of
-// 96 x 128), 128 x 256 (8 waves of 32 x 128) and 128 x 128 (4 waves of
-// 32 x 128): the tile grid is chosen per
+// 96 x 128), 192 x 128 (2 waves of 96 x 128), 128 x 256 (8 waves of 32 x 128)
+// and 128 x 128 (4 waves of 32 x 128): the tile grid is chosen per
 // problem by counting rounds of 256 workgroups, and every configuration
 // issues the same MFMA sequence per output element.
 constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
@@ -679,7 +679,8 @@ static bool use_mid(const QWeight& w, int m, int splits) {
 // kF16T256Tail: 256 x 256 tiles over the rows that fill whole rounds of 256
 // workgroups, then 128 x 256 tiles over the rest in a second launch.
 // kF16T384x256: 8 waves of 96 x 128, the whole 160 KB of LDS (two stages of
-// 384 + 256 rows of 128 bytes).
+// 384 + 256 rows of 128 bytes). kF16T192x128: 2 waves of 96 x 128 in 80 KB,
+// two workgroups per CU.
 enum F16Tile {
   kF16None = 0,
   kF16T256x256,
@@ -688,12 +689,21 @@ enum F16Tile {
   kF16T128x256,
   kF16T256Tail,
   kF16T128x128,
-  kF16T384x256
+  kF16T384x256,
+  kF16T192x128
 };
 static int f16_bm(int t) {
-  return t == kF16T384x256 ? 384 : t == kF16T192x256 ? 192 : (t == kF16T128x256 || t == kF16T128x128) ? 128 : 256;
+  return t == kF16T384x256                           ? 384
+         : (t == kF16T192x256 || t == kF16T192x128) ? 192
+         : (t == kF16T128x256 || t == kF16T128x128) ? 128
+                                                    : 256;
 }
-static int f16_bn(int t) { return (t == kF16T256x128 || t == kF16T128x128) ? 128 : 256; }
+static int f16_bn(int t) { return (t == kF16T256x128 || t == kF16T128x128 || t == kF16T192x128) ? 128 : 256; }
+
+// Rounds of 192 x 128 tiles: two workgroups fit on a CU, so a round is 512.
+static int rounds_192x128(const QWeight& w, int m, int splits) {
+  return (((m + 191) / 192) * (w.n / 128) * splits + 511) / 512;
+}
 
 // Rows of a kF16T256Tail launch's 256 x 256 part (n % 256 == 0).
 static int tail_main_rows(int m, int n) {
@@ -727,6 +737,11 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     // (104.6 us for the f16 GEMM against 127.5 on the tiling below).
     const int t384 = ((m + 383) / 384) * (w.n / 256) * splits;
     if (1525 * ((t384 + 255) / 256) < cost) best = kF16T384x256, cost = 1525 * ((t384 + 255) / 256);
+    // 192 x 128 tiles on 2 waves, two workgroups per CU: a round of 512
+    // charged 850 (f16 GEMM alone, random operands: the down projection's K
+    // split 4 ways at 1536 tokens 61.2 us against 61.7 on 192 x 256 tiles and
+    // 67.7 on 256 x 256).
+    if (850 * rounds_192x128(w, m, splits) < cost) best = kF16T192x128, cost = 850 * rounds_192x128(w, m, splits);
     // Whole rounds of 256-row tiles, then the rows left on 128-row tiles in
     // a second launch, a round of those charged 0.65 of a 256-row round.
     // With that charge the encoder's shapes pick the faster tiling (gate/up,
@@ -752,12 +767,17 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
     // 192 x 256 (128 x 256 81.0), at 1024 tokens 72.3 on 256 x 256; the QKV
     // projection's f16 GEMM at 1536 tokens 34.9 on 128 x 256 against 36.4 on
     // 128 x 128.
-    const int tiles[4] = {kF16T256x256, kF16T192x256, kF16T128x256, kF16T128x128};
-    const int charge[4] = {1000, 904, 650, 380};
+    // 192 x 128 tiles on 2 waves (two workgroups per CU, so a round is 512)
+    // charged 850 (f16 GEMM alone, random operands): the down projection's 2
+    // splits at 2400 tokens 91.8 us against 101.1 on 192 x 256, the attention
+    // output's 34.9 against 36.5.
+    const int tiles[5] = {kF16T256x256, kF16T192x256, kF16T128x256, kF16T128x128, kF16T192x128};
+    const int charge[5] = {1000, 904, 650, 380, 850};
+    const int slots[5] = {256, 256, 256, 256, 512};
     int best = kF16None, cost = 0;
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 5; ++i) {
       const int wg = ((m + f16_bm(tiles[i]) - 1) / f16_bm(tiles[i])) * (w.n / f16_bn(tiles[i])) * splits;
-      const int c = charge[i] * ((wg + 255) / 256);
+      const int c = charge[i] * ((wg + slots[i] - 1) / slots[i]);
       if (best == kF16None || c < cost) best = tiles[i], cost = c;
     }
     return best;
@@ -830,6 +850,7 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
     case kF16T128x256: launch_f16<256, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T128x128: launch_f16<128, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     case kF16T384x256: launch_f16<256, 4, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T192x128: launch_f16<128, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
