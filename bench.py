@@ -16,7 +16,8 @@ Printed JSON (one line on stdout):
   roofline     the dominant kernel (the Q4_K gate/up GEMM): algorithmic flops
                per launch / its average launch duration, from HIP events
                bracketing every launch on the plan's stream, against the dense
-               fp16 MFMA peak
+               fp16 MFMA peak (the weights' f16 expansion is done by the QKV
+               GEMM launch before it, on CUs that launch leaves idle)
   q4k_gemm_mfma_util
                that flop rate as % of the peak, next to the MFMA pipes' busy
                share of the same GEMM launches from hardware counters
@@ -654,7 +655,9 @@ def main() -> int:
         "projection_tflops": round(all_flops / (ms * 1e-3) / 1e12, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
-                     "kernel": "gate/up Q4_K dequant-matmul (expand + f16 MFMA GEMM, SwiGLU epilogue)",
+                     "kernel": "gate/up Q4_K dequant-matmul: the f16 MFMA GEMM launch(es), SwiGLU epilogue; the "
+                               "weights' Q4_K -> f16 expansion runs inside the preceding QKV GEMM launch on the CUs "
+                               "its tiles leave idle (timed in the qkv stage, part of every step)",
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "traffic_source": "profiles/gate_up_traffic_16x150.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)"},
     }

@@ -306,6 +306,11 @@ struct nemo_plan {
   std::mutex mu;
   DevPtr ids, x_full, norm_full, x_red, norm_red, qkv, attn, delta, ffn, out, rope, partials, wexp;
   size_t wexp_halves = 0;
+  // f16 expansions of a layer's gate/up and down weights, written by the QKV
+  // and O GEMM launches on the CUs their tiles leave idle (see
+  // gemm_f16_kernel), so the gate/up and down GEMMs start from them.
+  DevPtr wexp_gu, wexp_dn;
+  size_t wexp_gu_halves = 0, wexp_dn_halves = 0;
   // Rows of the last layer run (the attention's RoPE positions) and, made
   // on request, its rotated query and key heads.
   Ragged last_rows{};
@@ -804,6 +809,21 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     }
     if (wexp_halves) p->wexp = dev_alloc(wexp_halves * 2, "f16 weight expansion");
     p->wexp_halves = wexp_halves;
+    // Room for the gate/up and down expansions that ride on the QKV and O
+    // launches (Q4_K / Q6_K matrices that take the two-pass GEMM).
+    size_t gu = 0, dn = 0;
+    for (const LayerWeights& w : model->layers)
+      for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)}) {
+        if (m <= (size_t)kGemvMaxM) continue;
+        if (side_expand_of(w.gate_up, nullptr).type && gemm_two_pass(w.gate_up, (int)m, 1))
+          gu = std::max(gu, (size_t)w.gate_up.n * w.gate_up.k);
+        if (side_expand_of(w.down, nullptr).type && gemm_two_pass(w.down, (int)m, gemm_splits(w.down, (int)m)))
+          dn = std::max(dn, (size_t)w.down.n * w.down.k);
+      }
+    if (gu) p->wexp_gu = dev_alloc(gu * 2, "f16 gate/up expansion");
+    if (dn) p->wexp_dn = dev_alloc(dn * 2, "f16 down expansion");
+    p->wexp_gu_halves = gu;
+    p->wexp_dn_halves = dn;
     p->out = dev_alloc((size_t)batch * H * 4, "embeddings");
     const std::vector<float> table = rope_table(sequence, d.head_dim, d.rope_theta);
     p->rope = dev_alloc(table.size() * 4, "RoPE sin/cos table");
@@ -961,20 +981,35 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
       hip_check(launch_expand_q4k_pair(w.qkv.blocks, (int64_t)w.qkv.n * (w.qkv.k / 256), wexp, w.o.blocks,
                                        (int64_t)w.o.n * (w.o.k / 256), wexp_o, s),
                 "qkv/o expansion");
+    // The gate/up and down weights' f16 expansions ride on the QKV and O
+    // launches (their workgroups past the tiles; a launch that cannot carry
+    // them does them right after), when those GEMMs take the two-pass path.
+    const SideExpand side_gu =
+        !small && (size_t)w.gate_up.n * w.gate_up.k <= p->wexp_gu_halves && gemm_two_pass(w.gate_up, M, 1)
+            ? side_expand_of(w.gate_up, (uint16_t*)p->wexp_gu.get())
+            : SideExpand{};
+    const int down_splits = small ? 1 : gemm_splits(w.down, M);
+    const SideExpand side_dn =
+        !small && (size_t)w.down.n * w.down.k <= p->wexp_dn_halves && gemm_two_pass(w.down, M, down_splits)
+            ? side_expand_of(w.down, (uint16_t*)p->wexp_dn.get())
+            : SideExpand{};
     // One matrix, or separate q / k / v parts each into its column range.
-    auto qkv_proj = [&](const QWeight& wq, int col) {
+    auto qkv_proj = [&](const QWeight& wq, int col, const SideExpand* side) {
       const int sp = gemm_splits(wq, M);
       if (small) {
         hip_check(launch_gemv_ex(norm, H, wq, M, kEpiStore, qkv + col, QKV, partials, s), "qkv gemv");
       } else if (sp == 1) {
-        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp, pair), "qkv matmul");
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiStore, 1, qkv + col, QKV, s, wexp, pair, side), "qkv matmul");
       } else {
-        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s, wexp, pair), "qkv matmul");
+        hip_check(launch_gemm_ex(norm, H, wq, M, kEpiPartial, sp, partials, wq.n, s, wexp, pair, side),
+                  "qkv matmul");
         hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
       }
     };
-    if (w.qkv_parts.empty()) qkv_proj(w.qkv, 0);
-    for (const auto& part : w.qkv_parts) qkv_proj(part.first, part.second);
+    const SideExpand* gu_side = side_gu.type ? &side_gu : nullptr;
+    if (w.qkv_parts.empty()) qkv_proj(w.qkv, 0, gu_side);
+    for (size_t i = 0; i < w.qkv_parts.size(); ++i)
+      qkv_proj(w.qkv_parts[i].first, w.qkv_parts[i].second, i == 0 ? gu_side : nullptr);
     mark(2, false);
     mark(3, true);
     p->last_rows = rows;
@@ -994,7 +1029,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // Residual projection (O or down) then x += delta; RMSNorm. With a K
     // split, the norm kernel sums the fp32 partials itself.
     auto residual = [&](const uint16_t* in, int ldin, const QWeight& wt, const float* norm_w, int stage,
-                        uint16_t* wx, bool expanded) {
+                        uint16_t* wx, bool expanded, const SideExpand* side) {
       const int splits = small ? gemv_splits(wt) : gemm_splits(wt, M);
       mark(stage, true);
       if (small)
@@ -1002,9 +1037,10 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
                                  splits == 1 ? (void*)delta : (void*)partials, H, nullptr, s),
                   "residual gemv");
       else if (splits == 1)
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wx, expanded), "residual matmul");
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wx, expanded, side),
+                  "residual matmul");
       else
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wx, expanded),
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wx, expanded, side),
                   "residual matmul");
       mark(stage, false);
       mark(stage + 1, true);
@@ -1014,16 +1050,21 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
         hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
       mark(stage + 1, false);
     };
-    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair);
+    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_dn.type ? &side_dn : nullptr);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
     if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
+    } else if (side_gu.type) {
+      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, side_gu.out, true), "gate/up matmul");
     } else {
       hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     }
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
-    residual(ffn, F, w.down, next, 8, wexp, false);
+    if (side_dn.type)
+      residual(ffn, F, w.down, next, 8, side_dn.out, true, nullptr);
+    else
+      residual(ffn, F, w.down, next, 8, wexp, false, nullptr);
   }
   if (d.merge_after_layer == d.layers) {  // merge after the last layer (models shorter than the reference)
     mark(1, true);

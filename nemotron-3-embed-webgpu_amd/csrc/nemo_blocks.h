@@ -208,4 +208,94 @@ __device__ __forceinline__ void q40_expand(const Q40Fetch& f, half8v* lo, half8v
   hi[1] = to_half8(vh + 8);
 }
 
+// Q4_K raw: 8 threads per 144-byte block. Thread c writes output chunks c,
+// c + 8, c + 16, c + 24 of 8 values (values 64 i + 8 c .. +8 for group i),
+// so each store instruction of 8 neighbouring lanes fills 128 contiguous
+// bytes (f16) or 256 (f32): the low nibbles of bytes 8c .. 8c + 8 of every
+// group's 32 (c < 4) or the high nibbles of bytes 8(c - 4) .. (c >= 4).
+// NT: non-temporal stores, for output that is not read back soon.
+// Thread c (0..7) of the 144-byte block at `blk`, whose values start at
+// element o of the outputs.
+template <bool NT>
+__device__ __forceinline__ void q4k_block_part(const uint8_t* __restrict__ blk, int c, int64_t o0,
+                                               float* __restrict__ out32, uint16_t* __restrict__ out16) {
+  const int part = c & 3, high = c >> 2;
+  const u32x4 hdr = *(const u32x4*)blk;
+  uint32_t q[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 w = *(const uint2*)(blk + 16 + 32 * i + 8 * part);
+    q[i][0] = w.x;
+    q[i][1] = w.y;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float dsc0, ndm0, dsc1, ndm1;
+    q4k_group_factors(hdr, i, dsc0, ndm0, dsc1, ndm1);
+    const float dsc = high ? dsc1 : dsc0, ndm = high ? ndm1 : ndm0;
+    const int sh = 4 * high;
+    float v[8];
+    nibbles4_fma((q[i][0] >> sh) & 0x0f0f0f0fu, dsc, ndm, v);
+    nibbles4_fma((q[i][1] >> sh) & 0x0f0f0f0fu, dsc, ndm, v + 4);
+    const int64_t o = o0 + 64 * i + 8 * c;
+    if constexpr (NT) {
+      if (out32) {
+        __builtin_nontemporal_store(float4v{v[0], v[1], v[2], v[3]}, (float4v*)(out32 + o));
+        __builtin_nontemporal_store(float4v{v[4], v[5], v[6], v[7]}, (float4v*)(out32 + o + 4));
+      }
+      if (out16) __builtin_nontemporal_store(to_half8(v), (half8v*)(out16 + o));
+    } else {
+      if (out32) {
+        *(float4v*)(out32 + o) = float4v{v[0], v[1], v[2], v[3]};
+        *(float4v*)(out32 + o + 4) = float4v{v[4], v[5], v[6], v[7]};
+      }
+      if (out16) *(half8v*)(out16 + o) = to_half8(v);
+    }
+  }
+}
+
+// Q6_K split layout -> f16 (the two-pass GEMM's first pass), 8 threads per
+// 256-value block, thread c writing chunks c + 8 i of 8 values, so 8
+// neighbouring lanes fill 128 contiguous bytes per store. Value 64 i + 8 c + j
+// is (half h = i / 2, quadrant Q = 2 (i % 2) + c / 4, lane l = 8 (c % 4) + j)
+// (src/gguf/quantization.ts:53-71): its low bits are the low (Q < 2) or high
+// nibble of ql[64 h + 8 c + j], its high bits bits 2Q of
+// qh[32 h + 8 (c % 4) + j], its scale sc[8 h + (c % 4) / 2 + 2 Q]. `rec` is the
+// block's 208-byte record, `d_bits` its f16 scale, `out` its 256 values.
+__device__ __forceinline__ void q6k_block_part(const uint8_t* __restrict__ rec, uint16_t d_bits, int c,
+                                               uint16_t* __restrict__ out) {
+  uint2 ql[2], qh[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    ql[h] = *(const uint2*)(rec + 64 * h + 8 * c);
+    qh[h] = *(const uint2*)(rec + 128 + 32 * h + 8 * (c & 3));
+  }
+  const u32x4 sc = *(const u32x4*)(rec + 192);
+  const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+  const float d = h2f(d_bits);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = i >> 1, Q = 2 * (i & 1) + (c >> 2);
+    const int si = 8 * h + ((c & 3) >> 1) + 2 * Q;
+    const float dsc = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xffu);
+    const int ls = 4 * (i & 1), hs = 2 * Q;
+    const uint32_t w0 = ((ql[h].x >> ls) & 0x0f0f0f0fu) | (((qh[h].x >> hs) & 0x03030303u) << 4);
+    const uint32_t w1 = ((ql[h].y >> ls) & 0x0f0f0f0fu) | (((qh[h].y >> hs) & 0x03030303u) << 4);
+    float v[8];
+    bytes4_fma(opaque(w0), dsc, -32.0f * dsc, v);
+    bytes4_fma(opaque(w1), dsc, -32.0f * dsc, v + 4);
+    *(half8v*)(out + 64 * i + 8 * c) = to_half8(v);
+  }
+}
+
+// A matrix's Q4_K / Q6_K -> f16 expansion given to an f16 GEMM launch as side
+// work, done by the workgroups past the GEMM's tiles (see gemm_f16_kernel).
+// Thread c (0..7) of 256-value block b.
+__device__ __forceinline__ void side_expand_part(const SideExpand& e, int64_t b, int c) {
+  if (e.type == kQ4_K)
+    q4k_block_part<false>(e.blocks + b * 144, c, b * 256, nullptr, e.out);
+  else
+    q6k_block_part(e.blocks + b * 208, e.d[b], c, e.out + b * 256);
+}
+
 }  // namespace nemo

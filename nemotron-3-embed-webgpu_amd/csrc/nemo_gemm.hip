@@ -59,10 +59,11 @@ struct WFetch<kQ4_0> {
 
 // Epilogue for a wave owning MI x 4 blocks of 32 x 32 starting at (rbase0,
 // cbase): lane l, register r of block (i, j) is row rbase0 + 32i + 8(r/4) +
-// 4(l/32) + r%4, column cbase + 32j + l%32.
+// 4(l/32) + r%4, column cbase + 32j + l%32. `split`: the K split whose fp32
+// partials kEpiPartial writes.
 template <int EPI, int MI>
 __device__ __forceinline__ void gemm_epilogue(const float16v (&acc)[MI][4], int rbase0, int cbase, int lane, int M,
-                                              int N, void* out, int ldo) {
+                                              int N, void* out, int ldo, int split) {
   const int rbase = rbase0 + 4 * (lane >> 5);
   if constexpr (EPI == kEpiSwiGLU) {
     // Columns j*32 + l%32 (j = 0, 1) of this wave's 128 are gate features
@@ -98,7 +99,7 @@ __device__ __forceinline__ void gemm_epilogue(const float16v (&acc)[MI][4], int 
           if constexpr (EPI == kEpiStore)
             ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
           else
-            ((float*)out)[((size_t)blockIdx.z * M + row) * ldo + col] = acc[i][j][r];
+            ((float*)out)[((size_t)split * M + row) * ldo + col] = acc[i][j][r];
         }
       }
   }
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t* __restrict__ 
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
   }
-  gemm_epilogue<EPI, MI>(acc, m0 + wave * WM, n0, lane, M, N, out, ldo);
+  gemm_epilogue<EPI, MI>(acc, m0 + wave * WM, n0, lane, M, N, out, ldo, blockIdx.z);
 }
 
 // ---------------------------------------------------------------------------
@@ -455,7 +456,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(const uint16_t* __restric
   // The last (clamped, unused) copies must land before the workgroup's LDS
   // is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gemm_epilogue<EPI, MI>(acc, m0 + wm * 64, n0 + wn * 128, lane, M, N, out, ldo);
+  gemm_epilogue<EPI, MI>(acc, m0 + wm * 64, n0 + wn * 128, lane, M, N, out, ldo, blockIdx.z);
 }
 
 // ---------------------------------------------------------------------------
@@ -498,12 +499,27 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
 // issues the same MFMA sequence per output element.
 constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
 
+// The grid is one-dimensional: workgroup i < ntx * nty * ntz computes tile
+// (i % ntx, i / ntx % nty) of K split i / (ntx * nty) (the order a 3-D grid
+// would dispatch them in); the workgroups past the tiles do `side`, another
+// matrix's expansion, on the CUs the tiles leave idle (dispatched after the
+// tiles, so they never delay one).
 template <int EPI, int BN, int WM, int MI>
 __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
                                                                      const uint16_t* __restrict__ wt, int N, int K,
                                                                      int M, int kchunk, void* __restrict__ out,
-                                                                     int ldo) {
+                                                                     int ldo, int ntx, int nty, int ntiles,
+                                                                     SideExpand side) {
   constexpr int WAVES = WM * BN / 128, BM = 32 * MI * WM;
+  const int tile = blockIdx.x;
+  if (tile >= ntiles) {
+    constexpr int kPer = WAVES * 64 / 8;  // blocks per workgroup and round, 8 threads each
+    const int nside = gridDim.x - ntiles;
+    for (int64_t b = (int64_t)(tile - ntiles) * kPer + (threadIdx.x >> 3); b < side.nblocks; b += (int64_t)nside * kPer)
+      side_expand_part(side, b, (int)(threadIdx.x & 7));
+    return;
+  }
+  const int bx = tile % ntx, by = tile / ntx % nty, bz = tile / (ntx * nty);
   constexpr int XI = BM / 8 / WAVES, WI = BN / 8 / WAVES;  // copy instructions per wave and stage
   static_assert(XI * 8 * WAVES == BM && WI * 8 * WAVES == BN, "copies must cover the tiles");
   constexpr int XSTAGE = BM * 128, WSTAGE = BN * 128;
@@ -512,8 +528,8 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
   uint8_t* sW = smem + 2 * XSTAGE;  // [2][BN rows][128 B]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int kbeg = blockIdx.z * kchunk;
+  const int m0 = by * BM, n0 = bx * BN;
+  const int kbeg = bz * kchunk;
   const int nsteps = kchunk / kBK;
 
   // Each copy instruction moves 8 whole rows: lane l -> row R + l/8, slot
@@ -593,7 +609,7 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
     copy(1, kat(s + 3));
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo);
+  gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo, bz);
 }
 
 int gemm_splits(const QWeight& w, int m) {
@@ -797,15 +813,25 @@ bool gemm_two_pass(const QWeight& w, int m, int splits) {
 
 template <int BN, int WM, int MI>
 static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, const uint16_t* wexp, const QWeight& w,
-                       int m, int kchunk, void* out, int ldo, hipStream_t stream) {
-  constexpr int lds = f16_lds_bytes(32 * MI * WM, BN);
+                       int m, int kchunk, void* out, int ldo, hipStream_t stream, const SideExpand* side = nullptr) {
+  constexpr int lds = f16_lds_bytes(32 * MI * WM, BN), threads = WM * BN / 128 * 64;
+  const int ntiles = (int)(grid.x * grid.y * grid.z);
+  SideExpand e;
+  int nside = 0;
+  if (side && side->type && side->nblocks > 0) {
+    // Enough workgroups to cover the expansion in a few rounds (more than the
+    // CUs the tiles leave idle: the rest start as tiles finish).
+    e = *side;
+    nside = (int)std::min<int64_t>(1024, (e.nblocks + threads / 8 - 1) / (threads / 8));
+  }
   auto launch = [&](auto kernel) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
       (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
       configured = true;
     }
-    kernel<<<grid, WM * BN / 128 * 64, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo);
+    kernel<<<ntiles + nside, threads, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo, (int)grid.x,
+                                                      (int)grid.y, ntiles, e);
   };
   if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI>);
   else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI>);
@@ -814,7 +840,7 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
 
 static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
                                   void* out, int ldo, uint16_t* wexp, hipStream_t stream, int tile,
-                                  bool expanded = false) {
+                                  bool expanded = false, const SideExpand* side = nullptr) {
   const int bm = f16_bm(tile), bn = f16_bn(tile);
   if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
@@ -838,19 +864,20 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
     case kF16T256Tail: {
       if (splits != 1) return hipErrorInvalidValue;
       const int main = tail_main_rows(m, w.n), rest = m - main;
-      launch_f16<256, 4, 2>(epilogue, dim3(w.n / 256, main / 256, 1), x, ldx, wexp, w, main, kchunk, out, ldo, stream);
+      launch_f16<256, 4, 2>(epilogue, dim3(w.n / 256, main / 256, 1), x, ldx, wexp, w, main, kchunk, out, ldo, stream,
+                            side);
       const size_t skip = (size_t)main * ldo * (epilogue == kEpiPartial ? 4 : 2);  // bytes of the rows done
       launch_f16<256, 4, 1>(epilogue, dim3(w.n / 256, (rest + 127) / 128, 1), x + (size_t)main * ldx, ldx, wexp, w,
                             rest, kchunk, (uint8_t*)out + skip, ldo, stream);
       break;
     }
-    case kF16T256x256: launch_f16<256, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T256x128: launch_f16<128, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T192x256: launch_f16<256, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T128x256: launch_f16<256, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T128x128: launch_f16<128, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T384x256: launch_f16<256, 4, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
-    case kF16T192x128: launch_f16<128, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream); break;
+    case kF16T256x256: launch_f16<256, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T256x128: launch_f16<128, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T192x256: launch_f16<256, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T128x256: launch_f16<256, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T128x128: launch_f16<128, 4, 1>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T384x256: launch_f16<256, 4, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
+    case kF16T192x128: launch_f16<128, 2, 3>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -858,8 +885,8 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
 
 static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,
                                void* out, int ldo, hipStream_t stream, uint16_t* wexp, int forced,
-                               bool expanded = false) {
-  if (m <= 0) return hipSuccess;
+                               bool expanded = false, const SideExpand* side = nullptr) {
+  if (m <= 0) return side ? launch_side_expand(*side, stream) : hipSuccess;
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
   if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
@@ -868,7 +895,7 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   if (forced < 0 && use_mid(w, m, splits)) forced = kVarMid;
   const int tile = (wexp && forced < 0) ? two_pass_tile(w, m, splits) : kF16None;
   if (tile != kF16None)
-    return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile, expanded);
+    return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile, expanded, side);
   const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
 #define NEMO_LAUNCH(T)                                                                                              \
   if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
@@ -882,12 +909,14 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
     NEMO_LAUNCH(kQ4_0)
   }
 #undef NEMO_LAUNCH
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !side) return e;
+  return launch_side_expand(*side, stream);  // the fused kernels carry no side work
 }
 
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream, uint16_t* wexp, bool expanded) {
-  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, wexp, -1, expanded);
+                          int ldo, hipStream_t stream, uint16_t* wexp, bool expanded, const SideExpand* side) {
+  return launch_fused(x, ldx, w, m, epilogue, splits, out, ldo, stream, wexp, -1, expanded, side);
 }
 
 hipError_t launch_gemm_mid(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,

@@ -63,13 +63,34 @@ int gemm_splits(const QWeight& w, int m);
 // f16 MFMA GEMM (large batches) rather than decoding inside the GEMM.
 bool gemm_two_pass(const QWeight& w, int m, int splits);
 
+// Another matrix's Q4_K or Q6_K -> f16 expansion (row-major, the values
+// launch_expand_q4k / launch_expand_q6k write) carried by a GEMM launch:
+// the f16 GEMM's workgroups past its tiles do it on the CUs the tiles leave
+// idle. type 0: none.
+struct SideExpand {
+  int type = 0;
+  const uint8_t* blocks = nullptr;  // Q4_K blocks or Q6_K 208-byte records
+  const uint16_t* d = nullptr;      // Q6_K per-block scales
+  int64_t nblocks = 0;              // 256-value blocks
+  uint16_t* out = nullptr;          // nblocks * 256 halves
+};
+// The side work expanding `w` into `out`, or none (type 0) for a type it
+// does not cover (Q4_0, or a Q6_K matrix kept raw); with `out` null, only
+// whether it covers `w`.
+SideExpand side_expand_of(const QWeight& w, uint16_t* out);
+// The expansion alone, for a GEMM that cannot carry it.
+hipError_t launch_side_expand(const SideExpand& e, hipStream_t stream);
+
 // The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial. With
 // `wexp` (room for n * k halves) large problems take the two-pass path, whose
 // results are bit-identical to the fused kernels'. `expanded`: wexp already
 // holds w's f16 expansion (launch_expand_q4k_pair), which the two-pass path
-// then uses as it is.
+// then uses as it is. `side`: an expansion to do in the same launch (or, if
+// this GEMM does not take the two-pass path, right after it); it must not
+// write memory the GEMM reads.
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
-                          int ldo, hipStream_t stream, uint16_t* wexp = nullptr, bool expanded = false);
+                          int ldo, hipStream_t stream, uint16_t* wexp = nullptr, bool expanded = false,
+                          const SideExpand* side = nullptr);
 // Two Q4_K matrices' blocks -> f16, row-major, in one launch (each alone
 // would be latency-bound): n0 blocks of blocks0 to out0, n1 of blocks1 to out1.
 hipError_t launch_expand_q4k_pair(const uint8_t* blocks0, int64_t n0, uint16_t* out0, const uint8_t* blocks1,

@@ -543,52 +543,6 @@ hipError_t launch_gemv(const uint16_t* x, int ldx, const QWeight& w, uint16_t* y
 // Standalone decoding.
 // ---------------------------------------------------------------------------
 
-// Q4_K raw: 8 threads per 144-byte block. Thread c writes output chunks c,
-// c + 8, c + 16, c + 24 of 8 values (values 64 i + 8 c .. +8 for group i),
-// so each store instruction of 8 neighbouring lanes fills 128 contiguous
-// bytes (f16) or 256 (f32): the low nibbles of bytes 8c .. 8c + 8 of every
-// group's 32 (c < 4) or the high nibbles of bytes 8(c - 4) .. (c >= 4).
-// NT: non-temporal stores, for output that is not read back soon.
-// Thread c (0..7) of the 144-byte block at `blk`, whose values start at
-// element o of the outputs.
-template <bool NT>
-__device__ __forceinline__ void q4k_block_part(const uint8_t* __restrict__ blk, int c, int64_t o0,
-                                               float* __restrict__ out32, uint16_t* __restrict__ out16) {
-  const int part = c & 3, high = c >> 2;
-  const u32x4 hdr = *(const u32x4*)blk;
-  uint32_t q[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint2 w = *(const uint2*)(blk + 16 + 32 * i + 8 * part);
-    q[i][0] = w.x;
-    q[i][1] = w.y;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float dsc0, ndm0, dsc1, ndm1;
-    q4k_group_factors(hdr, i, dsc0, ndm0, dsc1, ndm1);
-    const float dsc = high ? dsc1 : dsc0, ndm = high ? ndm1 : ndm0;
-    const int sh = 4 * high;
-    float v[8];
-    nibbles4_fma((q[i][0] >> sh) & 0x0f0f0f0fu, dsc, ndm, v);
-    nibbles4_fma((q[i][1] >> sh) & 0x0f0f0f0fu, dsc, ndm, v + 4);
-    const int64_t o = o0 + 64 * i + 8 * c;
-    if constexpr (NT) {
-      if (out32) {
-        __builtin_nontemporal_store(float4v{v[0], v[1], v[2], v[3]}, (float4v*)(out32 + o));
-        __builtin_nontemporal_store(float4v{v[4], v[5], v[6], v[7]}, (float4v*)(out32 + o + 4));
-      }
-      if (out16) __builtin_nontemporal_store(to_half8(v), (half8v*)(out16 + o));
-    } else {
-      if (out32) {
-        *(float4v*)(out32 + o) = float4v{v[0], v[1], v[2], v[3]};
-        *(float4v*)(out32 + o + 4) = float4v{v[4], v[5], v[6], v[7]};
-      }
-      if (out16) *(half8v*)(out16 + o) = to_half8(v);
-    }
-  }
-}
-
 template <bool NT>
 __global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restrict__ raw, int64_t n_blocks,
                                                           float* __restrict__ out32, uint16_t* __restrict__ out16) {
@@ -730,36 +684,35 @@ __global__ __launch_bounds__(256) void expand_q6k_kernel(QWeight w, uint16_t* __
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t b = t >> 3;
   if (b >= (int64_t)w.n * (w.k >> 8)) return;
-  const int c = (int)(t & 7);
-  const uint8_t* rec = w.blocks + b * 208;
-  uint2 ql[2], qh[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    ql[h] = *(const uint2*)(rec + 64 * h + 8 * c);
-    qh[h] = *(const uint2*)(rec + 128 + 32 * h + 8 * (c & 3));
-  }
-  const u32x4 sc = *(const u32x4*)(rec + 192);
-  const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
-  const float d = h2f(w.d[b]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = i >> 1, Q = 2 * (i & 1) + (c >> 2);
-    const int si = 8 * h + ((c & 3) >> 1) + 2 * Q;
-    const float dsc = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xffu);
-    const int ls = 4 * (i & 1), hs = 2 * Q;
-    const uint32_t w0 = ((ql[h].x >> ls) & 0x0f0f0f0fu) | (((qh[h].x >> hs) & 0x03030303u) << 4);
-    const uint32_t w1 = ((ql[h].y >> ls) & 0x0f0f0f0fu) | (((qh[h].y >> hs) & 0x03030303u) << 4);
-    float v[8];
-    bytes4_fma(opaque(w0), dsc, -32.0f * dsc, v);
-    bytes4_fma(opaque(w1), dsc, -32.0f * dsc, v + 4);
-    *(half8v*)(out16 + b * 256 + 64 * i + 8 * c) = to_half8(v);
-  }
+  q6k_block_part(w.blocks + b * 208, w.d[b], (int)(t & 7), out16 + b * 256);
 }
 
 hipError_t launch_expand_q6k(const QWeight& w, uint16_t* out16, hipStream_t stream) {
   const int64_t threads = (int64_t)w.n * (w.k / 256) * 8;
   if (threads <= 0) return hipSuccess;
   expand_q6k_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(w, out16);
+  return hipGetLastError();
+}
+
+SideExpand side_expand_of(const QWeight& w, uint16_t* out) {
+  SideExpand e;
+  if (w.k % 256 || (w.type != kQ4_K && w.type != kQ6_K) || (w.type == kQ6_K && !w.d)) return e;
+  e.type = w.type;
+  e.blocks = w.blocks;
+  e.d = w.d;
+  e.nblocks = (int64_t)w.n * (w.k / 256);
+  e.out = out;
+  return e;
+}
+
+__global__ __launch_bounds__(256) void side_expand_kernel(SideExpand e) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if ((t >> 3) < e.nblocks) side_expand_part(e, t >> 3, (int)(t & 7));
+}
+
+hipError_t launch_side_expand(const SideExpand& e, hipStream_t stream) {
+  if (e.type == 0 || e.nblocks <= 0) return hipSuccess;
+  side_expand_kernel<<<(unsigned)((e.nblocks * 8 + 255) / 256), 256, 0, stream>>>(e);
   return hipGetLastError();
 }
 
