@@ -20,6 +20,9 @@
 // same f16 operands), so all paths give identical bits and a
 // token's result does not depend on how many other tokens share the batch.
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
 
 #include "nemo_blocks.h"
 #include "nemo_common.h"
@@ -499,16 +502,41 @@ __global__ __launch_bounds__(256) void expand_kernel(QWeight w, uint16_t* __rest
 // issues the same MFMA sequence per output element.
 constexpr int f16_lds_bytes(int bm, int bn) { return 2 * bm * 128 + 2 * bn * 128; }
 
-// The grid is one-dimensional: workgroup i < ntx * nty * ntz computes tile
-// (i % ntx, i / ntx % nty) of K split i / (ntx * nty) (the order a 3-D grid
-// would dispatch them in); the workgroups past the tiles do `side`, another
+// Tile (column bx, row by, K split bz) of workgroup i < ntiles = ntx nty ntz.
+// gw == 0: (i % ntx, i / ntx % nty, i / (ntx nty)), the order a 3-D grid
+// dispatches. gw > 0: workgroups go to the 8 XCDs round robin (i on XCD
+// i % 8), each with its own L2, so XCD x takes a contiguous run of tiles,
+// [x q + min(x, r), + q + (x < r)) for ntiles = 8 q + r, in an order that
+// keeps a run compact: K split outermost, then groups of gw column tiles
+// taken row by row. The XCDs then share fewer operand panels.
+__host__ __device__ inline void f16_tile_coords(int i, int ntx, int nty, int ntiles, int gw, int& bx, int& by,
+                                                int& bz) {
+  if (gw > 0) {
+    const int q = ntiles >> 3, r = ntiles & 7, x = i & 7;
+    i = x * q + (x < r ? x : r) + (i >> 3);
+  }
+  const int per = ntx * nty;
+  bz = i / per;
+  const int t = i - bz * per;
+  if (gw > 0) {
+    const int g = t / (gw * nty), c0 = g * gw, w = ntx - c0 < gw ? ntx - c0 : gw, u = t - g * gw * nty;
+    by = u / w;
+    bx = c0 + u % w;
+  } else {
+    bx = t % ntx;
+    by = t / ntx;
+  }
+}
+
+// The grid is one-dimensional: workgroup i < ntiles computes the tile that
+// f16_tile_coords gives it; the workgroups past the tiles do `side`, another
 // matrix's expansion, on the CUs the tiles leave idle (dispatched after the
 // tiles, so they never delay one).
 template <int EPI, int BN, int WM, int MI>
 __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
                                                                      const uint16_t* __restrict__ wt, int N, int K,
                                                                      int M, int kchunk, void* __restrict__ out,
-                                                                     int ldo, int ntx, int nty, int ntiles,
+                                                                     int ldo, int ntx, int nty, int ntiles, int gw,
                                                                      SideExpand side) {
   constexpr int WAVES = WM * BN / 128, BM = 32 * MI * WM;
   const int tile = blockIdx.x;
@@ -519,7 +547,8 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
       side_expand_part(side, b, (int)(threadIdx.x & 7));
     return;
   }
-  const int bx = tile % ntx, by = tile / ntx % nty, bz = tile / (ntx * nty);
+  int bx, by, bz;
+  f16_tile_coords(tile, ntx, nty, ntiles, gw, bx, by, bz);
   constexpr int XI = BM / 8 / WAVES, WI = BN / 8 / WAVES;  // copy instructions per wave and stage
   static_assert(XI * 8 * WAVES == BM && WI * 8 * WAVES == BN, "copies must cover the tiles");
   constexpr int XSTAGE = BM * 128, WSTAGE = BN * 128;
@@ -811,11 +840,59 @@ bool gemm_two_pass(const QWeight& w, int m, int splits) {
   return !use_mid(w, m, splits) && two_pass_tile(w, m, splits) != kF16None;
 }
 
+// Operand rows the XCDs' L2s fetch for one tile order: per XCD and round of
+// concurrent workgroups (slots over the chip), the distinct X row tiles times
+// bm plus the distinct W column tiles times bn, each per K split.
+static int64_t f16_order_rows(int ntx, int nty, int ntz, int bm, int bn, int slots, int gw) {
+  const int ntiles = ntx * nty * ntz, per_xcd = std::max(1, slots / 8);
+  std::vector<int> xs((size_t)nty * ntz, -1), ws((size_t)ntx * ntz, -1);
+  int64_t rows = 0;
+  for (int x = 0; x < 8; ++x)
+    for (int j = 0; x + 8 * j < ntiles; ++j) {
+      const int grp = x * (ntiles + 1) + j / per_xcd;
+      int bx, by, bz;
+      f16_tile_coords(x + 8 * j, ntx, nty, ntiles, gw, bx, by, bz);
+      int& sx = xs[(size_t)bz * nty + by];
+      int& sw = ws[(size_t)bz * ntx + bx];
+      if (sx != grp) sx = grp, rows += bm;
+      if (sw != grp) sw = grp, rows += bn;
+    }
+  return rows;
+}
+
+// Tile order of a launch (the gw of f16_tile_coords): the one whose XCDs
+// fetch the fewest operand rows, the dispatch order unless another saves at
+// least 5 %. The encoder's K-split projections gain most (the down
+// projection's 4 splits at 1536 tokens: every XCD reads all of X in the
+// dispatch order, 235 MB per launch, against 84 MB).
+static int f16_order(int ntx, int nty, int ntz, int bm, int bn, int slots) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int> memo;
+  const uint64_t key = (uint64_t)ntx | (uint64_t)nty << 16 | (uint64_t)ntz << 32 | (uint64_t)bm << 40 |
+                       (uint64_t)(bn / 128) << 50 | (uint64_t)(slots / 256) << 54;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto it = memo.find(key);
+  if (it != memo.end()) return it->second;
+  const int64_t base = f16_order_rows(ntx, nty, ntz, bm, bn, slots, 0);
+  int best = 0;
+  int64_t cost = base;
+  if (ntx * nty * ntz >= 16)
+    for (int g = 1; g <= ntx; ++g) {
+      const int64_t c = f16_order_rows(ntx, nty, ntz, bm, bn, slots, g);
+      if (c < cost) best = g, cost = c;
+    }
+  if (best && cost * 20 > base * 19) best = 0;
+  memo.emplace(key, best);
+  return best;
+}
+
 template <int BN, int WM, int MI>
 static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, const uint16_t* wexp, const QWeight& w,
                        int m, int kchunk, void* out, int ldo, hipStream_t stream, const SideExpand* side = nullptr) {
   constexpr int lds = f16_lds_bytes(32 * MI * WM, BN), threads = WM * BN / 128 * 64;
   const int ntiles = (int)(grid.x * grid.y * grid.z);
+  // two workgroups per CU for the 2-wave tiles
+  const int gw = f16_order((int)grid.x, (int)grid.y, (int)grid.z, 32 * MI * WM, BN, threads == 128 ? 512 : 256);
   SideExpand e;
   int nside = 0;
   if (side && side->type && side->nblocks > 0) {
@@ -831,7 +908,7 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
       configured = true;
     }
     kernel<<<ntiles + nside, threads, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo, (int)grid.x,
-                                                      (int)grid.y, ntiles, e);
+                                                      (int)grid.y, ntiles, gw, e);
   };
   if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI>);
   else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI>);
