@@ -188,7 +188,9 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
   constexpr int P = kGvTiles >= 2 ? kGvTiles / 2 : 1, G = kGvTiles >= 2 ? 4 / P : 8;
   static_assert(kGvWaves * 64 * 16 <= kGvXSlice, "a round's sums of a wave fit in its X region");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kGvWaves * kGvXSlice];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave index in a scalar register: the block and tile addresses below are
+  // then uniform and the loads take scalar bases with 32-bit lane offsets
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kq = lane >> 4, c = lane & 15;
   const int N = w.n, nblocks = w.k >> 8;
   const int n0 = kGvTiles >= 2 ? 128 * (blockIdx.x / G) + 16 * P * (blockIdx.x % G) : 16 * blockIdx.x;
@@ -207,12 +209,13 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
     // Registers, then LDS: the compiler orders the wave's own LDS write and
     // reads.
     half8v xs[8];
+    const uint8_t* xb = (const uint8_t*)(x + 256 * blk);  // uniform base, 32-bit lane offsets
     auto load_x = [&](int g) {
       const int t0 = lane >> 5, s = lane & 31;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int t = 2 * i + t0;
-        xs[i] = *(const half8v*)(x + (size_t)min(16 * g + t, M - 1) * ldx + 256 * blk + 8 * (s ^ t));
+        xs[i] = *(const half8v*)(xb + 2u * (uint32_t)(min(16 * g + t, M - 1) * ldx + 8 * (s ^ t)));
       }
     };
     load_x(0);
