@@ -1050,12 +1050,17 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
         hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
       mark(stage + 1, false);
     };
-    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_dn.type ? &side_dn : nullptr);
+    // The down expansion goes to the gate/up GEMM instead when that ends with
+    // a launch of rows left over from whole rounds (CUs idle there).
+    const bool dn_on_gu = side_dn.type && side_gu.type && gemm_two_pass_tail(w.gate_up, M, 1);
+    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_dn.type && !dn_on_gu ? &side_dn : nullptr);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
     if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
     } else if (side_gu.type) {
-      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, side_gu.out, true), "gate/up matmul");
+      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, side_gu.out, true,
+                               dn_on_gu ? &side_dn : nullptr),
+                "gate/up matmul");
     } else {
       hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     }

@@ -840,6 +840,10 @@ bool gemm_two_pass(const QWeight& w, int m, int splits) {
   return !use_mid(w, m, splits) && two_pass_tile(w, m, splits) != kF16None;
 }
 
+bool gemm_two_pass_tail(const QWeight& w, int m, int splits) {
+  return !use_mid(w, m, splits) && two_pass_tile(w, m, splits) == kF16T256Tail;
+}
+
 // Operand rows the XCDs' L2s fetch for one tile order: per XCD and round of
 // concurrent workgroups (slots over the chip), the distinct X row tiles times
 // bm plus the distinct W column tiles times bn, each per K split.
@@ -941,11 +945,11 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
     case kF16T256Tail: {
       if (splits != 1) return hipErrorInvalidValue;
       const int main = tail_main_rows(m, w.n), rest = m - main;
-      launch_f16<256, 4, 2>(epilogue, dim3(w.n / 256, main / 256, 1), x, ldx, wexp, w, main, kchunk, out, ldo, stream,
-                            side);
+      // side work on the second launch, whose tiles leave CUs idle
+      launch_f16<256, 4, 2>(epilogue, dim3(w.n / 256, main / 256, 1), x, ldx, wexp, w, main, kchunk, out, ldo, stream);
       const size_t skip = (size_t)main * ldo * (epilogue == kEpiPartial ? 4 : 2);  // bytes of the rows done
       launch_f16<256, 4, 1>(epilogue, dim3(w.n / 256, (rest + 127) / 128, 1), x + (size_t)main * ldx, ldx, wexp, w,
-                            rest, kchunk, (uint8_t*)out + skip, ldo, stream);
+                            rest, kchunk, (uint8_t*)out + skip, ldo, stream, side);
       break;
     }
     case kF16T256x256: launch_f16<256, 4, 2>(epilogue, grid, x, ldx, wexp, w, m, kchunk, out, ldo, stream, side); break;

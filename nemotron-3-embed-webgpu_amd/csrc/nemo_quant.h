@@ -62,6 +62,10 @@ int gemm_splits(const QWeight& w, int m);
 // Whether launch_gemm_ex, given scratch, expands `w` to f16 before an f16 x
 // f16 MFMA GEMM (large batches) rather than decoding inside the GEMM.
 bool gemm_two_pass(const QWeight& w, int m, int splits);
+// Whether that two-pass GEMM ends with a launch of 128-row tiles for the rows
+// left after whole rounds of 256-row tiles, which leaves CUs idle (side work
+// given to such a GEMM goes to that launch).
+bool gemm_two_pass_tail(const QWeight& w, int m, int splits);
 
 // Another matrix's Q4_K or Q6_K -> f16 expansion (row-major, the values
 // launch_expand_q4k / launch_expand_q6k write) carried by a GEMM launch:
