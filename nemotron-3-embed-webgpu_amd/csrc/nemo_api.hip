@@ -815,9 +815,9 @@ nemo_status nemo_plan_create(nemo_model* model, int32_t batch, int32_t sequence,
     for (const LayerWeights& w : model->layers)
       for (const size_t m : {tf, std::min<size_t>(tf, kLargeM - 1)}) {
         if (m <= (size_t)kGemvMaxM) continue;
-        if (side_expand_of(w.gate_up, nullptr).type && gemm_two_pass(w.gate_up, (int)m, 1))
+        if (side_part_of(w.gate_up, nullptr).type && gemm_two_pass(w.gate_up, (int)m, 1))
           gu = std::max(gu, (size_t)w.gate_up.n * w.gate_up.k);
-        if (side_expand_of(w.down, nullptr).type && gemm_two_pass(w.down, (int)m, gemm_splits(w.down, (int)m)))
+        if (side_part_of(w.down, nullptr).type && gemm_two_pass(w.down, (int)m, gemm_splits(w.down, (int)m)))
           dn = std::max(dn, (size_t)w.down.n * w.down.k);
       }
     if (gu) p->wexp_gu = dev_alloc(gu * 2, "f16 gate/up expansion");
@@ -984,15 +984,27 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // The gate/up and down weights' f16 expansions ride on the QKV and O
     // launches (their workgroups past the tiles; a launch that cannot carry
     // them does them right after), when those GEMMs take the two-pass path.
-    const SideExpand side_gu =
+    const SidePart part_gu =
         !small && (size_t)w.gate_up.n * w.gate_up.k <= p->wexp_gu_halves && gemm_two_pass(w.gate_up, M, 1)
-            ? side_expand_of(w.gate_up, (uint16_t*)p->wexp_gu.get())
-            : SideExpand{};
+            ? side_part_of(w.gate_up, (uint16_t*)p->wexp_gu.get())
+            : SidePart{};
     const int down_splits = small ? 1 : gemm_splits(w.down, M);
-    const SideExpand side_dn =
+    const SidePart part_dn =
         !small && (size_t)w.down.n * w.down.k <= p->wexp_dn_halves && gemm_two_pass(w.down, M, down_splits)
-            ? side_expand_of(w.down, (uint16_t*)p->wexp_dn.get())
-            : SideExpand{};
+            ? side_part_of(w.down, (uint16_t*)p->wexp_dn.get())
+            : SidePart{};
+    // The down expansion goes to the gate/up GEMM when that ends with a
+    // launch of rows left over from whole rounds (CUs idle there), else to
+    // the O launch. The gate/up expansion is shared: its first 3/4 on the
+    // QKV launch, the rest on the O launch (16 x 150 tokens, measured with
+    // 200-pass runs: 0.6-0.8 % faster per pass than all of it on the QKV
+    // launch; 0.55 and 0.85 of it on the QKV launch did less well).
+    const bool dn_on_gu = part_dn.type && part_gu.type && gemm_two_pass_tail(w.gate_up, M, 1);
+    const int64_t nq = part_gu.nblocks * 3 / 4;
+    SideExpand side_q, side_o, side_t;
+    side_q.add(side_part_range(part_gu, 0, nq));
+    side_o.add(side_part_range(part_gu, nq, part_gu.nblocks - nq));
+    (dn_on_gu ? side_t : side_o).add(part_dn);
     // One matrix, or separate q / k / v parts each into its column range.
     auto qkv_proj = [&](const QWeight& wq, int col, const SideExpand* side) {
       const int sp = gemm_splits(wq, M);
@@ -1006,7 +1018,7 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
         hip_check(launch_reduce_partials(partials, sp, M, wq.n, qkv + col, QKV, s), "qkv reduce");
       }
     };
-    const SideExpand* gu_side = side_gu.type ? &side_gu : nullptr;
+    const SideExpand* gu_side = side_q.count ? &side_q : nullptr;
     if (w.qkv_parts.empty()) qkv_proj(w.qkv, 0, gu_side);
     for (size_t i = 0; i < w.qkv_parts.size(); ++i)
       qkv_proj(w.qkv_parts[i].first, w.qkv_parts[i].second, i == 0 ? gu_side : nullptr);
@@ -1050,24 +1062,21 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
         hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
       mark(stage + 1, false);
     };
-    // The down expansion goes to the gate/up GEMM instead when that ends with
-    // a launch of rows left over from whole rounds (CUs idle there).
-    const bool dn_on_gu = side_dn.type && side_gu.type && gemm_two_pass_tail(w.gate_up, M, 1);
-    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_dn.type && !dn_on_gu ? &side_dn : nullptr);
+    residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_o.count ? &side_o : nullptr);
     mark(6, true);  // gate/up GEMM with SwiGLU in its epilogue
     if (small) {
       hip_check(launch_gemv_ex(norm, H, w.gate_up, M, kEpiSwiGLU, ffn, F, partials, s), "gate/up gemv");
-    } else if (side_gu.type) {
-      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, side_gu.out, true,
-                               dn_on_gu ? &side_dn : nullptr),
+    } else if (part_gu.type) {
+      hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, part_gu.out, true,
+                               side_t.count ? &side_t : nullptr),
                 "gate/up matmul");
     } else {
       hip_check(launch_gemm_ex(norm, H, w.gate_up, M, kEpiSwiGLU, 1, ffn, F, s, wexp), "gate/up matmul");
     }
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
-    if (side_dn.type)
-      residual(ffn, F, w.down, next, 8, side_dn.out, true, nullptr);
+    if (part_dn.type)
+      residual(ffn, F, w.down, next, 8, part_dn.out, true, nullptr);
     else
       residual(ffn, F, w.down, next, 8, wexp, false, nullptr);
   }

@@ -291,11 +291,20 @@ __device__ __forceinline__ void q6k_block_part(const uint8_t* __restrict__ rec, 
 // A matrix's Q4_K / Q6_K -> f16 expansion given to an f16 GEMM launch as side
 // work, done by the workgroups past the GEMM's tiles (see gemm_f16_kernel).
 // Thread c (0..7) of 256-value block b.
+// Block b counts over the parts in order; each field is picked by value
+// (no copy of a part that the compiler would index in private memory).
 __device__ __forceinline__ void side_expand_part(const SideExpand& e, int64_t b, int c) {
-  if (e.type == kQ4_K)
-    q4k_block_part<false>(e.blocks + b * 144, c, b * 256, nullptr, e.out);
-  else
-    q6k_block_part(e.blocks + b * 208, e.d[b], c, e.out + b * 256);
+  const bool second = e.count > 1 && b >= e.part[0].nblocks;
+  if (second) b -= e.part[0].nblocks;
+  const int type = second ? e.part[1].type : e.part[0].type;
+  const uint8_t* blocks = second ? e.part[1].blocks : e.part[0].blocks;
+  uint16_t* out = second ? e.part[1].out : e.part[0].out;
+  if (type == kQ4_K) {
+    q4k_block_part<false>(blocks + b * 144, c, b * 256, nullptr, out);
+  } else {
+    const uint16_t* d = second ? e.part[1].d : e.part[0].d;
+    q6k_block_part(blocks + b * 208, d[b], c, out + b * 256);
+  }
 }
 
 }  // namespace nemo

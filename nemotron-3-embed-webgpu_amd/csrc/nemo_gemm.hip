@@ -899,7 +899,7 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
   const int gw = f16_order((int)grid.x, (int)grid.y, (int)grid.z, 32 * MI * WM, BN, threads == 128 ? 512 : 256);
   SideExpand e;
   int nside = 0;
-  if (side && side->type && side->nblocks > 0) {
+  if (side && side->count && side->nblocks > 0) {
     // Enough workgroups to cover the expansion in a few rounds (more than the
     // CUs the tiles leave idle: the rest start as tiles finish).
     e = *side;

@@ -67,22 +67,40 @@ bool gemm_two_pass(const QWeight& w, int m, int splits);
 // given to such a GEMM goes to that launch).
 bool gemm_two_pass_tail(const QWeight& w, int m, int splits);
 
-// Another matrix's Q4_K or Q6_K -> f16 expansion (row-major, the values
-// launch_expand_q4k / launch_expand_q6k write) carried by a GEMM launch:
-// the f16 GEMM's workgroups past its tiles do it on the CUs the tiles leave
-// idle. type 0: none.
-struct SideExpand {
+// Blocks [first, first + nblocks) of a matrix's Q4_K or Q6_K -> f16
+// expansion (row-major, the values launch_expand_q4k / launch_expand_q6k
+// write). type 0: none.
+struct SidePart {
   int type = 0;
-  const uint8_t* blocks = nullptr;  // Q4_K blocks or Q6_K 208-byte records
-  const uint16_t* d = nullptr;      // Q6_K per-block scales
+  const uint8_t* blocks = nullptr;  // the range's Q4_K blocks or Q6_K 208-byte records
+  const uint16_t* d = nullptr;      // Q6_K per-block scales of the range
   int64_t nblocks = 0;              // 256-value blocks
   uint16_t* out = nullptr;          // nblocks * 256 halves
 };
-// The side work expanding `w` into `out`, or none (type 0) for a type it
-// does not cover (Q4_0, or a Q6_K matrix kept raw); with `out` null, only
-// whether it covers `w`.
-SideExpand side_expand_of(const QWeight& w, uint16_t* out);
-// The expansion alone, for a GEMM that cannot carry it.
+// Up to kMaxParts such ranges carried by a GEMM launch: the f16 GEMM's
+// workgroups past its tiles do them on the CUs the tiles leave idle, the
+// parts' blocks numbered one after another.
+struct SideExpand {
+  static constexpr int kMaxParts = 2;
+  int count = 0;
+  int64_t nblocks = 0;  // over all parts
+  SidePart part[kMaxParts];
+  // Appends p (nothing for an empty part); false when the parts are full.
+  bool add(const SidePart& p) {
+    if (!p.type || p.nblocks <= 0) return true;
+    if (count == kMaxParts) return false;
+    part[count++] = p;
+    nblocks += p.nblocks;
+    return true;
+  }
+};
+// The expansion of `w` into `out`, or none (type 0) for a type it does not
+// cover (Q4_0, or a Q6_K matrix kept raw); with `out` null, only whether it
+// covers `w`.
+SidePart side_part_of(const QWeight& w, uint16_t* out);
+// Blocks [first, first + count) of p.
+SidePart side_part_range(const SidePart& p, int64_t first, int64_t count);
+// The expansions alone, for a GEMM that cannot carry them.
 hipError_t launch_side_expand(const SideExpand& e, hipStream_t stream);
 
 // The MFMA GEMM with an epilogue; `splits` > 1 only with kEpiPartial. With

@@ -2,6 +2,7 @@
 // wavefront GEMV (m <= 160), GGML Q4_K / Q6_K / Q4_0 block decoding to
 // float32/f16 (bit-exact with src/gguf/quantization.ts:19-74), and the
 // fixed-order reduction of split-K partial sums.
+#include <algorithm>
 #include <type_traits>
 
 #include "nemo_blocks.h"
@@ -697,8 +698,18 @@ hipError_t launch_expand_q6k(const QWeight& w, uint16_t* out16, hipStream_t stre
   return hipGetLastError();
 }
 
-SideExpand side_expand_of(const QWeight& w, uint16_t* out) {
-  SideExpand e;
+SidePart side_part_range(const SidePart& p, int64_t first, int64_t count) {
+  SidePart r = p;
+  first = std::max<int64_t>(0, std::min(first, p.nblocks));
+  r.nblocks = std::max<int64_t>(0, std::min(count, p.nblocks - first));
+  r.blocks = p.blocks + first * (p.type == kQ4_K ? 144 : 208);
+  if (p.d) r.d = p.d + first;
+  r.out = p.out + first * 256;
+  return r;
+}
+
+SidePart side_part_of(const QWeight& w, uint16_t* out) {
+  SidePart e;
   if (w.k % 256 || (w.type != kQ4_K && w.type != kQ6_K) || (w.type == kQ6_K && !w.d)) return e;
   e.type = w.type;
   e.blocks = w.blocks;
@@ -714,7 +725,7 @@ __global__ __launch_bounds__(256) void side_expand_kernel(SideExpand e) {
 }
 
 hipError_t launch_side_expand(const SideExpand& e, hipStream_t stream) {
-  if (e.type == 0 || e.nblocks <= 0) return hipSuccess;
+  if (e.count == 0 || e.nblocks <= 0) return hipSuccess;
   side_expand_kernel<<<(unsigned)((e.nblocks * 8 + 255) / 256), 256, 0, stream>>>(e);
   return hipGetLastError();
 }
