@@ -17,7 +17,9 @@ Printed JSON (one line on stdout):
                per launch / its average launch duration, from HIP events
                bracketing every launch on the plan's stream, against the dense
                fp16 MFMA peak (the weights' f16 expansion is done by the QKV
-               GEMM launch before it, on CUs that launch leaves idle)
+               and O GEMM launches before it, on CUs those launches leave
+               idle; at 2400 tokens its own second launch expands the down
+               weights the same way, and that time counts here)
   q4k_gemm_mfma_util
                that flop rate as % of the peak, next to the MFMA pipes' busy
                share of the same GEMM launches from hardware counters
@@ -656,8 +658,9 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": committed_traffic(),
                      "kernel": "gate/up Q4_K dequant-matmul: the f16 MFMA GEMM launch(es), SwiGLU epilogue; the "
-                               "weights' Q4_K -> f16 expansion runs inside the preceding QKV GEMM launch on the CUs "
-                               "its tiles leave idle (timed in the qkv stage, part of every step)",
+                               "weights' Q4_K -> f16 expansion runs inside the preceding QKV and O GEMM launches on "
+                               "the CUs their tiles leave idle (timed in those stages, part of every step); at 2400 "
+                               "tokens the second launch also expands the down weights on its idle CUs (counted here)",
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "traffic_source": "profiles/gate_up_traffic_16x150.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)"},
     }
