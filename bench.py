@@ -410,7 +410,8 @@ def kernel_rates(torch, stream) -> dict:
                 weight copies totalling more than the 256 MB Infinity Cache;
       dequant   Q4_K blocks -> f16, (bytes read + bytes written) / time;
       cpu       the same dequant-matmul by the reference's CPU check restated
-                (dequantize each row, float64 dot; oracle, one thread)."""
+                (dequantize each row, float64 dot; oracle, one thread, and the
+                same on every host thread of the process with OpenMP)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -458,6 +459,21 @@ def kernel_rates(torch, stream) -> dict:
     out["cpu_q4k_matmul_15x2048x2048"] = {"ms_per_call": round(cpu_ms, 2), "cores": 1, "kind": "port",
                                           "gbs": round(2482176 / (cpu_ms * 1e-3) / 1e9, 2)}
     log(f"cpu dequant-matmul: {cpu_ms:.1f} ms per call")
+    # the same on every host thread the box gives this process (C restatement, OpenMP)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+    single = oracle.q4k_matmul_cpu(raw, x16, 15, 2048, 2048)
+    assert np.array_equal(oracle.q4k_matmul_cpu_mt(raw, x16, 15, 2048, 2048, threads), single)
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < 2.0:
+        oracle.q4k_matmul_cpu_mt(raw, x16, 15, 2048, 2048, threads)
+        reps += 1
+    mt_ms = (time.perf_counter() - t0) * 1e3 / reps
+    out["cpu_q4k_matmul_15x2048x2048_all_cores"] = {
+        "ms_per_call": round(mt_ms, 3), "cores": threads, "kind": "port",
+        "label": f"C restatement, {threads} cores (OpenMP, same bits as the 1-core run)",
+        "gbs": round(2482176 / (mt_ms * 1e-3) / 1e9, 2)}
+    log(f"cpu dequant-matmul on {threads} threads: {mt_ms:.2f} ms per call")
     return out
 
 

@@ -16,6 +16,7 @@
  * even). We do exactly that: compute in double, cast once to float.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -244,6 +245,29 @@ double oracle_q4k_matmul_cpu(const uint8_t* w, const float* x, int64_t m, int64_
       double expected = 0;
       const float* xr = x + i * k;
       for (int64_t t = 0; t < k; ++t) expected += (double)xr[t] * (double)row_scratch[t];
+      out[i * n + j] = expected;
+      checksum += expected;
+    }
+  }
+  return checksum;
+}
+
+/* The same computation spread over `threads` OpenMP threads by weight row
+ * (each row's outputs computed exactly as above, so the results are the same
+ * bits); the all-cores variant of the CPU baseline. row_scratch holds
+ * threads * k floats. */
+double oracle_q4k_matmul_cpu_mt(const uint8_t* w, const float* x, int64_t m, int64_t n, int64_t k, int threads,
+                                float* row_scratch, double* out) {
+  const int64_t blocks = k / 256;
+  double checksum = 0;
+#pragma omp parallel for num_threads(threads) schedule(static) reduction(+ : checksum)
+  for (int64_t j = 0; j < n; ++j) {
+    float* row = row_scratch + (int64_t)omp_get_thread_num() * k;
+    oracle_dequant_q4k(w + j * blocks * 144, blocks, row);
+    for (int64_t i = 0; i < m; ++i) {
+      double expected = 0;
+      const float* xr = x + i * k;
+      for (int64_t t = 0; t < k; ++t) expected += (double)xr[t] * (double)row[t];
       out[i * n + j] = expected;
       checksum += expected;
     }

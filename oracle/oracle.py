@@ -112,6 +112,9 @@ def lib() -> ctypes.CDLL:
     L.oracle_matmul_f64.argtypes = [f32p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, f64p]
     L.oracle_q4k_matmul_cpu.restype = ctypes.c_double
     L.oracle_q4k_matmul_cpu.argtypes = [u8p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, f32p, f64p]
+    L.oracle_q4k_matmul_cpu_mt.restype = ctypes.c_double
+    L.oracle_q4k_matmul_cpu_mt.argtypes = [u8p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                           f32p, f64p]
     _lib = L
     return L
 
@@ -209,6 +212,18 @@ def q4k_matmul_cpu(w_raw: np.ndarray, x: np.ndarray, m: int, n: int, k: int) -> 
     out = np.empty((m, n), dtype=np.float64)
     lib().oracle_q4k_matmul_cpu(_ptr(w, ctypes.c_uint8), _ptr(xf, ctypes.c_float), m, n, k,
                                 _ptr(scratch, ctypes.c_float), _ptr(out, ctypes.c_double))
+    return out
+
+
+def q4k_matmul_cpu_mt(w_raw: np.ndarray, x: np.ndarray, m: int, n: int, k: int, threads: int) -> np.ndarray:
+    """q4k_matmul_cpu spread over `threads` OpenMP threads by weight row, each
+    output computed by the same loop (same bits): the all-cores CPU baseline."""
+    w = np.ascontiguousarray(w_raw.reshape(-1).view(np.uint8))
+    xf = np.ascontiguousarray(x.astype(np.float32).reshape(m, k))
+    scratch = np.empty(threads * k, dtype=np.float32)
+    out = np.empty((m, n), dtype=np.float64)
+    lib().oracle_q4k_matmul_cpu_mt(_ptr(w, ctypes.c_uint8), _ptr(xf, ctypes.c_float), m, n, k, int(threads),
+                                   _ptr(scratch, ctypes.c_float), _ptr(out, ctypes.c_double))
     return out
 
 
