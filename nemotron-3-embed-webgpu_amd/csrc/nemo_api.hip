@@ -953,6 +953,15 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
   hip_check(launch_rmsnorm(x_full, nullptr, m->layers[0].attn_norm, norm_full, src.start[src.count], H, d.rms_epsilon, s),
             "rmsnorm");
   mark(0, false);
+  // Whether layer l's QKV and O weights are expanded together into wexp (QKV,
+  // then O), and the layer whose expansion the previous down launch did.
+  auto pair_of = [&](int l) {
+    const LayerWeights& w = m->layers[l];
+    const Ragged& rows = l < d.merge_after_layer ? src : dst;
+    return expand_qkv_o_together(w, rows.start[rows.count]) &&
+           (size_t)w.qkv.n * w.qkv.k + (size_t)w.o.n * w.o.k <= p->wexp_halves;
+  };
+  int pair_done = -1;
   for (int l = 0; l < d.layers; ++l) {
     if (l == d.merge_after_layer) {
       mark(1, true);
@@ -974,10 +983,9 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // depend on the rest of the batch.
     const bool small = M <= kGemvMaxM;
     // QKV and O expanded together: QKV at wexp, O after it.
-    const bool pair = expand_qkv_o_together(w, M) &&
-                      (size_t)w.qkv.n * w.qkv.k + (size_t)w.o.n * w.o.k <= p->wexp_halves;
+    const bool pair = !small && pair_of(l);
     uint16_t* wexp_o = pair ? wexp + (size_t)w.qkv.n * w.qkv.k : wexp;
-    if (pair)
+    if (pair && pair_done != l)
       hip_check(launch_expand_q4k_pair(w.qkv.blocks, (int64_t)w.qkv.n * (w.qkv.k / 256), wexp, w.o.blocks,
                                        (int64_t)w.o.n * (w.o.k / 256), wexp_o, s),
                 "qkv/o expansion");
@@ -1075,9 +1083,19 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     }
     mark(6, false);
     const float* next = l + 1 < d.layers ? m->layers[l + 1].attn_norm : m->output_norm;
-    if (part_dn.type)
-      residual(ffn, F, w.down, next, 8, part_dn.out, true, nullptr);
-    else
+    if (part_dn.type) {
+      // The next layer's QKV and O expansion rides on the down launch (its
+      // workgroups past the tiles fill the CUs as the tiles finish): that
+      // GEMM reads its own expansion, not wexp, which no later kernel of
+      // this layer touches.
+      SideExpand side_n;
+      if (l + 1 < d.layers && pair_of(l + 1)) {
+        const LayerWeights& w1 = m->layers[l + 1];
+        const SidePart q1 = side_part_of(w1.qkv, wexp), o1 = side_part_of(w1.o, wexp + (size_t)w1.qkv.n * w1.qkv.k);
+        if (q1.type && o1.type && side_n.add(q1) && side_n.add(o1)) pair_done = l + 1;
+      }
+      residual(ffn, F, w.down, next, 8, part_dn.out, true, side_n.count ? &side_n : nullptr);
+    } else
       residual(ffn, F, w.down, next, 8, wexp, false, nullptr);
   }
   if (d.merge_after_layer == d.layers) {  // merge after the last layer (models shorter than the reference)
