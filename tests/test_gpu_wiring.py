@@ -164,3 +164,29 @@ def test_key_sampling_rule_before_and_after_the_merge(torch_cuda, dense_before_m
         c = W.cos(got[0], want)
         assert c >= 0.99999, f"layer {layer}: cosine {c}"
         assert W.cos(got[0], mutant) < c - 1e-5, f"layer {layer}"
+
+
+@pytest.mark.parametrize("thr, ids, keys0, keys4", W.KEY_RULE_BOUNDARY)
+def test_key_sampling_rule_at_the_threshold(torch_cuda, thr, ids, keys0, keys4):
+    """The attention kernel's key rule at the threshold itself, against the
+    same closed forms as the oracle (tests/test_oracle_wiring.py): exactly
+    `threshold` states attend every key, one more every third, judged on the
+    layer's own state count after the merge."""
+    from dataclasses import replace
+    d = replace(D, kv_stride_threshold=thr, kv_dense_before_merge=0)
+    rd = dims()
+    rd.kv_stride_threshold = thr
+    emb = W.embedding_table()
+    norms = W.random_norms(130, D.layers)
+    w_out = (1.0 + 0.4 * synth.normal(131, H)).astype(np.float32)
+    n, n4 = len(ids), -(-len(ids) * 16 // 25)
+    for layer, keys, states in ((0, keys0, n), (4, keys4, n4)):
+        m = W.uniform_passthrough_model(emb, norms, w_out, layer, d)
+        got, _ = run(tensors_for(m), [ids], rd)
+        want = W.uniform_closed_form(emb, ids, norms, w_out, layer, list(keys))
+        other = range(states) if list(keys) != list(range(states)) else range(0, states, 3)
+        mutant = W.uniform_closed_form(emb, ids, norms, w_out, layer, list(other))
+        c = W.cos(got[0], want)
+        assert c >= 0.99999, f"layer {layer}: cosine {c}"
+        assert W.cos(got[0], mutant) < c - 1e-5, f"layer {layer}"
+

@@ -81,8 +81,11 @@ def cos(a, b):
 
 # merge bins worked out by hand from src/webgpu/ops.ts:648-654
 # (start = 1 + ((p-1)(S-1)) // (T-1), end = 1 + (p(S-1)) // (T-1)):
-# S = 3 -> T = 2: [0,1) [1,3); S = 7 -> T = 5: [0,1) [1,2) [2,4) [4,5) [5,7)
-BINS = {2: [(0, 1), (1, 2)], 3: [(0, 1), (1, 3)], 7: [(0, 1), (1, 2), (2, 4), (4, 5), (5, 7)]}
+# S = 3 -> T = 2: [0,1) [1,3); S = 7 -> T = 5: [0,1) [1,2) [2,4) [4,5) [5,7);
+# S = 5 -> T = 4 (S-1 = 4, T-1 = 3): [0,1) [1,2) [2,3) [3,5);
+# S = 6 -> T = 4 (S-1 = 5, T-1 = 3): [0,1) [1,2) [2,4) [4,6)
+BINS = {2: [(0, 1), (1, 2)], 3: [(0, 1), (1, 3)], 5: [(0, 1), (1, 2), (2, 3), (3, 5)],
+        6: [(0, 1), (1, 2), (2, 4), (4, 6)], 7: [(0, 1), (1, 2), (2, 4), (4, 5), (5, 7)]}
 
 
 def merged(rows16, S):
@@ -304,3 +307,38 @@ def test_key_sampling_rule_before_and_after_the_merge(dense_before_merge):
         assert np.allclose(got, want, atol=1e-7, rtol=0), f"layer {layer}"
         mutant = uniform_closed_form(emb, ids, norms, w_out, layer, list(other))
         assert cos(mutant, want) < 1 - 1e-4, f"layer {layer}: the other key set gives the same embedding"
+
+
+# Threshold, request ids, keys attended in layer 0 (before the merge) and in
+# layer 4 (after it, ceil(0.64 n) states) under the code's rule: a request
+# exactly as long as the threshold attends every key (ops.ts:258 compares
+# valid_length > threshold), one state longer attends every third.
+KEY_RULE_BOUNDARY = [
+    (5, [2, 7, 11, 19, 23], range(5), range(4)),           # 5 states = threshold: dense; 4 after the merge
+    (5, [2, 7, 11, 19, 23, 29], [0, 3], range(4)),         # 6 > 5: every third; 4 after the merge: dense
+    (4, [2, 7, 11, 19, 23, 29], [0, 3], range(4)),         # 6 > 4 before; 4 = threshold after the merge: dense
+    (3, [2, 7, 11, 19, 23, 29], [0, 3], [0, 3]),           # 4 > 3 after the merge too: every third
+]
+
+
+@pytest.mark.parametrize("thr, ids, keys0, keys4", KEY_RULE_BOUNDARY)
+def test_key_sampling_rule_at_the_threshold(thr, ids, keys0, keys4):
+    """The threshold itself: a layer whose request holds exactly `threshold`
+    states attends all of them, one more state switches to every third key.
+    A rule with >= instead of > fails the first and third cases, one that
+    counts tokens before the merge in later layers fails the third."""
+    from dataclasses import replace
+    d = replace(D, kv_stride_threshold=thr, kv_dense_before_merge=0)
+    emb = embedding_table()
+    norms = random_norms(130, D.layers)
+    w_out = (1.0 + 0.4 * synth.normal(131, H)).astype(np.float32)
+    n, n4 = len(ids), -(-len(ids) * 16 // 25)
+    for layer, keys, states in ((0, keys0, n), (4, keys4, n4)):
+        m = uniform_passthrough_model(emb, norms, w_out, layer, d)
+        want = uniform_closed_form(emb, ids, norms, w_out, layer, list(keys))
+        got = oracle.forward_request(m, np.array(ids))
+        assert np.allclose(got, want, atol=1e-7, rtol=0), f"layer {layer}"
+        other = range(states) if list(keys) != list(range(states)) else range(0, states, 3)
+        mutant = uniform_closed_form(emb, ids, norms, w_out, layer, list(other))
+        assert cos(mutant, want) < 1 - 1e-4, f"layer {layer}: the other key set gives the same embedding"
+

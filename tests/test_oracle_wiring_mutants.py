@@ -10,7 +10,11 @@ the named pin then fails:
 * attn_norm and ffn_norm exchanged after the attention output (model.ts:130);
 * pre-merge positions for RoPE after the merge (src/webgpu/ops.ts:188);
 * pooling the residual stream (model.ts:138 pools the normalized one);
-* merging only the residual stream (model.ts:159 merges both).
+* merging only the residual stream (model.ts:159 merges both);
+* every third key from `threshold` states on instead of above it
+  (src/webgpu/ops.ts:258 compares valid_length > threshold);
+* the key rule judged on the request's tokens before the merge in the
+  layers after it.
 """
 import inspect
 import textwrap
@@ -41,6 +45,14 @@ MUTANTS = {
         "    return mean_pool(norm, T)",
         "    return mean_pool(x, T)",
         "test_zero_projections_pool_the_output_normalized_merged_rows"),
+    "threshold compared with >=": (
+        "att = attention(q, k, v, d, n if dense else d.kv_stride_threshold, d.kv_stride)",
+        "att = attention(q, k, v, d, n if dense else d.kv_stride_threshold - 1, d.kv_stride)",
+        "test_key_sampling_rule_at_the_threshold"),
+    "key rule on the tokens before the merge": (
+        "att = attention(q, k, v, d, n if dense else d.kv_stride_threshold, d.kv_stride)",
+        "att = attention(q, k, v, d, n if dense else d.kv_stride_threshold - (S - n), d.kv_stride)",
+        "test_key_sampling_rule_at_the_threshold"),
     "merge only the residual stream": (
         "            norm = merge(norm, S, T)\n",
         "            norm = norm[[b[0] for b in merge_bins(S, T)]]\n",
@@ -51,7 +63,9 @@ MUTANTS = {
 def _cases(test):
     for mark in getattr(test, "pytestmark", []):
         if mark.name == "parametrize":
-            return [(v,) for v in mark.args[1]]
+            names = mark.args[0]
+            multi = "," in names if isinstance(names, str) else len(names) > 1
+            return [tuple(v) if multi else (v,) for v in mark.args[1]]
     return [()]
 
 
