@@ -223,6 +223,26 @@ def test_plan_errors_mirror_reference(torch_cuda):
     assert len(out) == 2 and all(abs(np.linalg.norm(e) - 1) < 0.01 for e in out)
 
 
+def test_largest_batch_of_tiny_and_ragged_requests(torch_cuda):
+    """The most requests a plan takes (64) in one pass, lengths from one
+    token up, every one against the oracle; 65 requests are refused."""
+    dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, layers=3, vocab=300,
+                        merge_after_layer=2)
+    tensors = synth.model_tensors(dims, seed=646)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    lengths = [[1, 2, 3, 4, 7, 15, 33, 64, 100, 160, 161, 5][i % 12] for i in range(64)]
+    seqs = [[1] + list(synth.randint(5000 + i, n - 1, 2, 300)) for i, n in enumerate(lengths)]
+    ids, lens = _padded(seqs, max(lengths))
+    got = model.createPlan(64, max(lengths)).run_sync(ids, lens)
+    assert len(got) == 64
+    for i, s in enumerate(seqs):
+        c = _cos(got[i], oracle.forward_request(om, np.array(s)))
+        assert c >= 0.9999, f"request {i} (len {len(s)}): cosine {c:.6f}"
+    with pytest.raises(rt.NemoError, match="batch must be in"):
+        model.createPlan(65, 4)
+
+
 def test_missing_tensor_is_named(torch_cuda):
     dims = rt.make_dims(hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=256, layers=1, vocab=50,
                         merge_after_layer=1)
