@@ -982,16 +982,18 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
     // depend on the pass size, so within a regime a token's result does not
     // depend on the rest of the batch.
     const bool small = M <= kGemvMaxM;
-    // QKV and O expanded together: QKV at wexp, O after it.
+    // QKV and O expanded together: QKV at wexp, O after it (by the previous
+    // layer's down launch, or by a launch of its own here).
     const bool pair = !small && pair_of(l);
     uint16_t* wexp_o = pair ? wexp + (size_t)w.qkv.n * w.qkv.k : wexp;
     if (pair && pair_done != l)
       hip_check(launch_expand_q4k_pair(w.qkv.blocks, (int64_t)w.qkv.n * (w.qkv.k / 256), wexp, w.o.blocks,
                                        (int64_t)w.o.n * (w.o.k / 256), wexp_o, s),
                 "qkv/o expansion");
-    // The gate/up and down weights' f16 expansions ride on the QKV and O
-    // launches (their workgroups past the tiles; a launch that cannot carry
-    // them does them right after), when those GEMMs take the two-pass path.
+    // The gate/up and down weights' f16 expansions, when those GEMMs take the
+    // two-pass path, ride on earlier GEMM launches of the layer (their
+    // workgroups past the tiles; a launch that cannot carry them does them
+    // right after).
     const SidePart part_gu =
         !small && (size_t)w.gate_up.n * w.gate_up.k <= p->wexp_gu_halves && gemm_two_pass(w.gate_up, M, 1)
             ? side_part_of(w.gate_up, (uint16_t*)p->wexp_gu.get())
