@@ -877,15 +877,19 @@ static int f16_order(int ntx, int nty, int ntz, int bm, int bn, int slots) {
   std::lock_guard<std::mutex> lock(mu);
   const auto it = memo.find(key);
   if (it != memo.end()) return it->second;
-  const int64_t base = f16_order_rows(ntx, nty, ntz, bm, bn, slots, 0);
+  // Group widths tried: 1..16, the larger powers of two and ntx (the cost
+  // of one is linear in the tiles; very large grids keep the dispatch order).
+  const int64_t ntiles = (int64_t)ntx * nty * ntz;
   int best = 0;
-  int64_t cost = base;
-  if (ntx * nty * ntz >= 16)
-    for (int g = 1; g <= ntx; ++g) {
+  if (ntiles >= 16 && ntiles <= 65536) {
+    const int64_t base = f16_order_rows(ntx, nty, ntz, bm, bn, slots, 0);
+    int64_t cost = base;
+    for (int g = 1; g <= ntx; g = g < 16 ? g + 1 : (g * 2 > ntx && g != ntx ? ntx : g * 2)) {
       const int64_t c = f16_order_rows(ntx, nty, ntz, bm, bn, slots, g);
       if (c < cost) best = g, cost = c;
     }
-  if (best && cost * 20 > base * 19) best = 0;
+    if (best && cost * 20 > base * 19) best = 0;
+  }
   memo.emplace(key, best);
   return best;
 }
