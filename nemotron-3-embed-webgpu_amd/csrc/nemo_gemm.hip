@@ -202,16 +202,28 @@ template <int TYPE, int EPI>
 // (x is not __restrict__: a restrict read-only pointer's loads may move across
 // the compiler fences below.)
 __global__ __launch_bounds__(256) void gemm_mid_kernel(const uint16_t* x, int ldx, QWeight w, int M,
-                                                       int kchunk, void* __restrict__ out, int ldo) {
+                                                       int kchunk, void* __restrict__ out, int ldo, int ntx, int nty,
+                                                       int ntiles, SideExpand side) {
   constexpr int BM = kMidBM, BN = 128, D = kMidDepth;
   static_assert(D % 2 == 0, "the LDS buffer of step s + u is u % 2");
   __shared__ __attribute__((aligned(16))) half_t sA[2][BM * kLdsK];
   __shared__ __attribute__((aligned(16))) half_t sB[2][BN * kLdsK];
+  // One-dimensional grid: workgroup i < ntiles computes tile (i % ntx,
+  // i / ntx % nty) of K split i / (ntx nty); the workgroups past the tiles
+  // do `side` (as gemm_f16_kernel's).
+  const int tile = blockIdx.x;
+  if (tile >= ntiles) {
+    const int nside = gridDim.x - ntiles;
+    for (int64_t b = (int64_t)(tile - ntiles) * 32 + (threadIdx.x >> 3); b < side.nblocks; b += (int64_t)nside * 32)
+      side_expand_part(side, b, (int)(threadIdx.x & 7));
+    return;
+  }
+  const int bx = tile % ntx, by = tile / ntx % nty, bz = tile / (ntx * nty);
   const int N = w.n;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int kbeg = blockIdx.z * kchunk;
+  const int m0 = by * BM, n0 = bx * BN;
+  const int kbeg = bz * kchunk;
   const int nsteps = kchunk / kBK;
   const size_t row_bytes = qweight_row_bytes(TYPE, w.k);
 
@@ -309,7 +321,7 @@ __global__ __launch_bounds__(256) void gemm_mid_kernel(const uint16_t* x, int ld
         if constexpr (EPI == kEpiStore)
           ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[j][r]);
         else
-          ((float*)out)[((size_t)blockIdx.z * M + row) * ldo + col] = acc[j][r];
+          ((float*)out)[((size_t)bz * M + row) * ldo + col] = acc[j][r];
       }
     }
   }
@@ -672,8 +684,9 @@ int mid_splits(const QWeight& w) {
 enum GemmVariant { kVarBig = 0, kVarLds128 = 1, kVarLds256 = 2, kVarMid = 3 };
 
 template <int TYPE, int EPI>
-static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx, const QWeight& w, int kchunk,
-                         void* out, int ldo, hipStream_t s) {
+// Returns whether the launch carried `side` (only the 64-row tiles do).
+static bool launch_typed(int var, int m, int splits, const uint16_t* x, int ldx, const QWeight& w, int kchunk,
+                         void* out, int ldo, hipStream_t s, const SideExpand* side) {
   if (var == kVarBig) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
@@ -684,8 +697,15 @@ static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx,
     dim3 grid((w.n + kBigBN - 1) / kBigBN, (m + kBigBM - 1) / kBigBM, splits);
     gemm_big_kernel<TYPE, EPI><<<grid, 512, kBigLds, s>>>(x, ldx, w, m, kchunk, out, ldo);
   } else if (var == kVarMid && (kchunk / kBK) % kMidDepth == 0) {
-    dim3 grid((w.n + 127) / 128, (m + kMidBM - 1) / kMidBM, splits);
-    gemm_mid_kernel<TYPE, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
+    const int ntx = (w.n + 127) / 128, nty = (m + kMidBM - 1) / kMidBM, ntiles = ntx * nty * splits;
+    SideExpand e;
+    int nside = 0;
+    if (side && side->count && side->nblocks > 0) {
+      e = *side;
+      nside = (int)std::min<int64_t>(1024, (e.nblocks + 31) / 32);  // 32 blocks per workgroup and round
+    }
+    gemm_mid_kernel<TYPE, EPI><<<ntiles + nside, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo, ntx, nty, ntiles, e);
+    return nside > 0;
   } else if (var == kVarLds256) {
     dim3 grid((w.n + 127) / 128, (m + 255) / 256, splits);
     gemm_kernel<TYPE, 256, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
@@ -693,6 +713,7 @@ static void launch_typed(int var, int m, int splits, const uint16_t* x, int ldx,
     dim3 grid((w.n + 127) / 128, (m + 127) / 128, splits);
     gemm_kernel<TYPE, 128, EPI><<<grid, 256, 0, s>>>(x, ldx, w, m, kchunk, out, ldo);
   }
+  return false;
 }
 
 // Fused-kernel choice, from measurements of the encoder's shapes: the 256 x
@@ -982,10 +1003,14 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   if (tile != kF16None)
     return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile, expanded, side);
   const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
-#define NEMO_LAUNCH(T)                                                                                              \
-  if (epilogue == kEpiStore) launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);       \
-  else if (epilogue == kEpiPartial) launch_typed<T, kEpiPartial>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream); \
-  else launch_typed<T, kEpiSwiGLU>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream);
+  bool carried = false;
+#define NEMO_LAUNCH(T)                                                                                               \
+  if (epilogue == kEpiStore)                                                                                         \
+    carried = launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);                \
+  else if (epilogue == kEpiPartial)                                                                                  \
+    carried = launch_typed<T, kEpiPartial>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);              \
+  else                                                                                                               \
+    carried = launch_typed<T, kEpiSwiGLU>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);
   if (w.type == kQ4_K) {
     NEMO_LAUNCH(kQ4_K)
   } else if (w.type == kQ6_K) {
@@ -995,8 +1020,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   }
 #undef NEMO_LAUNCH
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !side) return e;
-  return launch_side_expand(*side, stream);  // the fused kernels carry no side work
+  if (e != hipSuccess || !side || carried) return e;
+  return launch_side_expand(*side, stream);  // the other fused kernels carry no side work
 }
 
 hipError_t launch_gemm_ex(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits, void* out,
