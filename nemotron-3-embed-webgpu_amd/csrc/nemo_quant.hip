@@ -520,6 +520,8 @@ hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
   if (m <= 0) return hipSuccess;
   if (m > kGemvMaxM || (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0)) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
+  // The kernel addresses X with 32-bit byte offsets.
+  if (ldx < w.k || 2 * ((int64_t)(m - 1) * ldx + w.k) > INT32_MAX) return hipErrorInvalidValue;
   const int splits = gemv_splits(w);
   if (epilogue == kEpiPartial) {
     // [splits][m][n] fp32 sums into `out` (row stride n)
