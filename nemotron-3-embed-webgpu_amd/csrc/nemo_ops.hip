@@ -381,10 +381,20 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  // m: the query's reference maximum (log2 units, scaled); lsum: the sum of
+  // this half's probabilities (the two halves' are added at the end).
   float m = -INFINITY, lsum = 0.f;
 
   // One block of kAttnKeys staged keys from key kb of cK [keys][KP] and
   // cV [HD][vp]; keys at or past `staged` are masked.
+  //
+  // Probabilities are taken against a reference maximum m that is raised
+  // only when a query's block maximum exceeds it by more than 2^8 (a wave
+  // vote): p = 2^(s - m) <= 256 then, exact enough in f16 and far from
+  // overflow in the fp32 sums, and the common block needs no cross-lane
+  // exchange, no rescale of the accumulators and no 2^(m - m') of its own.
+  // The result is the softmax all the same: numerator and denominator share
+  // the reference.
   auto block = [&](const half_t* cK, const half_t* cV, int vp, int kb, int staged) {
     // S^T block: lane holds query l%32, key kb + 8(r/4) + 4hl + r%4.
     float16v s;
@@ -395,30 +405,34 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
       const half8v a = *(const half8v*)&cK[(kb + (lane & 31)) * KP + 16 * c + 8 * hl];
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
     }
-    float bm = -INFINITY;
+    if (kb + kAttnKeys > staged) {  // the request's last keys: mask past its end
+      asm volatile("");  // keeps this rare path a branch (not computed and selected every block)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-      s[r] = key < staged ? s[r] * scale2 : -INFINITY;
-      bm = fmaxf(bm, s[r]);
+      for (int r = 0; r < 16; ++r)
+        if (kb + 8 * (r >> 2) + 4 * hl + (r & 3) >= staged) s[r] = -INFINITY;
     }
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mn = fmaxf(m, bm);
-    const float alpha = exp2f(m - mn);
-    float ps = 0.f;
+    float bm = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+    bm *= scale2;  // scale2 > 0: the maximum of the scaled scores
+    if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {
+      asm volatile("");
+      const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      m = mn;
+    }
     float p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = exp2f(s[r] - mn);
-      ps += p[r];
+      // v_exp_f32 itself: results below 2^-126 (flushed) add nothing to the sums
+      p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], scale2, -m));
+      lsum += p[r];
     }
-    ps += __shfl_xor(ps, 32, 64);
-    lsum = lsum * alpha + ps;
-    m = mn;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
     // O^T += V^T P^T over two 16-key chunks: MFMA k slot 8hl + e of chunk c2
     // is key 16c2 + 8(e/4) + 4hl + e%4 = score register 8c2 + e.
 #pragma unroll
@@ -526,6 +540,7 @@ __global__ __launch_bounds__(512) void attention_kernel(const uint16_t* __restri
       for (int kb = 0; kb < staged; kb += kAttnKeys) block(sK, sVt, VP, kb, staged);
     }
   }
+  lsum += __shfl_xor(lsum, 32, 64);  // the two halves' keys (same references)
   if (qi >= n) return;
   const float inv = 1.0f / lsum;
   uint16_t* op = out + ((size_t)(row0 + qi) * q_heads + h) * HD;
