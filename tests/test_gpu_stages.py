@@ -114,3 +114,41 @@ def test_config2_one_layer_at_config_dims(torch_cuda):
     assert cos >= 0.9999, f"cosine {cos}"
     plan.destroy()
     model.destroy()
+
+
+@pytest.mark.parametrize("hd,n", [(64, 200), (64, 300), (128, 100), (128, 200)])
+def test_attention_with_widely_spread_scores(torch_cuda, hd, n):
+    """The attention's softmax keeps a reference maximum per query and raises
+    it only when a 32-key block's maximum passes it by more than 2^8 (log2
+    units). Weights of spread 0.12 (scores spanning ~45-50 log2 units) make
+    the later blocks raise it, which the test first confirms on the oracle's
+    own q and k, then checks the attention stage and the embedding against
+    the oracle: keys staged all at once (200 tokens at head_dim 64, 100 at
+    128) and in prepared 32-key rounds (300 and 200)."""
+    H, V, F = 256, 300, 512
+    Hq, Hkv = (4, 2) if hd == 64 else (2, 1)
+    dims = rt.make_dims(hidden=H, q_heads=Hq, kv_heads=Hkv, head_dim=hd, intermediate=F, layers=1, vocab=V,
+                        merge_after_layer=1)
+    tensors = synth.model_tensors(dims, seed=700 + hd + n, sigma=0.12)
+    model = rt.NemotronHipModel(tensors, dims=dims)
+    om = synth.oracle_model(dims, tensors)
+    seq = np.array([1] + list(synth.randint(43 + n, n - 1, 2, V)), dtype=np.uint32)
+    plan = model.createPlan(1, n)
+    got = plan.run_sync(seq, [n])[0]
+    trace = {}
+    ref = oracle.forward_request(om, seq.astype(np.int64), trace)
+    q = np.asarray(trace["q"][0], np.float64).reshape(n, Hq, hd)
+    k = np.asarray(trace["k"][0], np.float64).reshape(n, Hkv, hd)
+    raised = 0
+    for h in range(Hq):
+        s = q[:, h] @ k[:, h // (Hq // Hkv)].T / np.sqrt(hd) * np.log2(np.e)   # [query, key], log2 units
+        ref_max = s[:, :32].max(axis=1)
+        for b in range(32, n, 32):
+            blk = s[:, b:b + 32].max(axis=1)
+            raised += int(np.count_nonzero(blk > ref_max + 8))
+            ref_max = np.where(blk > ref_max + 8, np.maximum(ref_max, blk), ref_max)
+    assert raised > 0, "the scores never pass the reference maximum by 2^8: the test would not reach that path"
+    att = _rel(plan.read_buffer("attention")[: n * Hq * hd], trace["attention"][0])
+    assert att <= 1e-2, f"attention relative error {att} ({raised} raises)"
+    cos = float(np.dot(got, ref) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    assert cos >= 0.9999, f"cosine {cos}"
