@@ -1061,15 +1061,19 @@ static void enqueue_graph(nemo_plan* p, const uint32_t* d_ids, const Ragged& src
       else if (splits == 1)
         hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiStore, 1, delta, H, s, wx, expanded, side),
                   "residual matmul");
-      else
-        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial, splits, partials, H, s, wx, expanded, side),
+      else  // K split over the tiles: each split's sum stored as f16, half the bytes of fp32 partials
+        hip_check(launch_gemm_ex(in, ldin, wt, M, kEpiPartial16, splits, partials, H, s, wx, expanded, side),
                   "residual matmul");
       mark(stage, false);
       mark(stage + 1, true);
       if (splits == 1)
         hip_check(launch_rmsnorm(x, delta, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
-      else
+      else if (small)
         hip_check(launch_rmsnorm_partials(x, partials, splits, norm_w, norm, M, H, d.rms_epsilon, s), "rmsnorm");
+      else
+        hip_check(launch_rmsnorm_partials16(x, (const uint16_t*)partials, splits, norm_w, norm, M, H, d.rms_epsilon,
+                                            s),
+                  "rmsnorm");
       mark(stage + 1, false);
     };
     residual(attn, QW, w.o, w.ffn_norm, 4, wexp_o, pair, side_o.count ? &side_o : nullptr);

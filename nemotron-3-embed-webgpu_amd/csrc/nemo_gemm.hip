@@ -101,6 +101,8 @@ __device__ __forceinline__ void gemm_epilogue(const float16v (&acc)[MI][4], int 
           if (row >= M) continue;
           if constexpr (EPI == kEpiStore)
             ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
+          else if constexpr (EPI == kEpiPartial16)
+            ((uint16_t*)out)[((size_t)split * M + row) * ldo + col] = f2h(acc[i][j][r]);
           else
             ((float*)out)[((size_t)split * M + row) * ldo + col] = acc[i][j][r];
         }
@@ -320,6 +322,8 @@ __global__ __launch_bounds__(256) void gemm_mid_kernel(const uint16_t* x, int ld
         if (row >= M) continue;
         if constexpr (EPI == kEpiStore)
           ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[j][r]);
+        else if constexpr (EPI == kEpiPartial16)
+          ((uint16_t*)out)[((size_t)bz * M + row) * ldo + col] = f2h(acc[j][r]);
         else
           ((float*)out)[((size_t)bz * M + row) * ldo + col] = acc[j][r];
       }
@@ -941,6 +945,7 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
   };
   if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI>);
   else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI>);
+  else if (epilogue == kEpiPartial16) launch(gemm_f16_kernel<kEpiPartial16, BN, WM, MI>);
   else launch(gemm_f16_kernel<kEpiSwiGLU, BN, WM, MI>);
 }
 
@@ -994,7 +999,7 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
                                bool expanded = false, const SideExpand* side = nullptr) {
   if (m <= 0) return side ? launch_side_expand(*side, stream) : hipSuccess;
   if (splits < 1 || (w.k / 256) % splits) return hipErrorInvalidValue;
-  if (epilogue != kEpiPartial && splits != 1) return hipErrorInvalidValue;
+  if (epilogue != kEpiPartial && epilogue != kEpiPartial16 && splits != 1) return hipErrorInvalidValue;
   if (epilogue == kEpiSwiGLU && w.n % 128) return hipErrorInvalidValue;
   if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
@@ -1009,6 +1014,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
     carried = launch_typed<T, kEpiStore>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);                \
   else if (epilogue == kEpiPartial)                                                                                  \
     carried = launch_typed<T, kEpiPartial>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);              \
+  else if (epilogue == kEpiPartial16)                                                                                \
+    carried = launch_typed<T, kEpiPartial16>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);            \
   else                                                                                                               \
     carried = launch_typed<T, kEpiSwiGLU>(var, m, splits, x, ldx, w, kchunk, out, ldo, stream, side);
   if (w.type == kQ4_K) {

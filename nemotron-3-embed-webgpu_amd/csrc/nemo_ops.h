@@ -22,6 +22,10 @@ hipError_t launch_rmsnorm(uint16_t* x, const uint16_t* delta, const float* w, ui
 // The same with delta = f16(sum over s of partials[s][row][:]) (split order).
 hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int splits, const float* w,
                                    uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream);
+// The same with f16 partials (kEpiPartial16: each split's fp32 sum rounded
+// once), widened and added in split order; splits 2 to 4.
+hipError_t launch_rmsnorm_partials16(uint16_t* x, const uint16_t* partials, int splits, const float* w,
+                                     uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream);
 
 // Rotate adjacent pairs of the query and key heads of qkv into q [t, Hq, hd]
 // and k [t, Hkv, hd]; position = row index within its request; table =

@@ -100,7 +100,8 @@ hipError_t launch_embed(const uint32_t* ids, int padded_seq, const Ragged& rows,
 // added in split order); kAnySplits: the same for a run-time count.
 constexpr int kAnySplits = 1000;
 
-template <int DELTA>
+// H16: the partials are f16 (kEpiPartial16), widened to fp32 before the sum.
+template <int DELTA, bool H16 = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, const void* __restrict__ delta,
                                                       int splits, int rows, const float* __restrict__ w,
                                                       uint16_t* __restrict__ out, int hidden, float eps) {
@@ -111,7 +112,22 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ x, 
     half8v xv = *(const half8v*)(x + base + c);
     if constexpr (DELTA != 0) {
       float dv[8];
-      if constexpr (DELTA > 0) {
+      if constexpr (DELTA > 0 && H16) {
+        const uint16_t* p = (const uint16_t*)delta + base + c;
+        const size_t slice = (size_t)rows * hidden;
+        half8v ph[DELTA];
+#pragma unroll
+        for (int s = 0; s < DELTA; ++s) ph[s] = *(const half8v*)(p + s * slice);
+        float a[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (float)ph[0][i];
+#pragma unroll
+        for (int s = 1; s < DELTA; ++s)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a[i] += (float)ph[s][i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dv[i] = (float)(half_t)a[i];
+      } else if constexpr (DELTA > 0) {
         const float* p = (const float*)delta + base + c;
         const size_t slice = (size_t)rows * hidden;
         float4v a, b;
@@ -193,6 +209,21 @@ hipError_t launch_rmsnorm_partials(uint16_t* x, const float* partials, int split
     default: NEMO_NORM(kAnySplits); break;
   }
 #undef NEMO_NORM
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_partials16(uint16_t* x, const uint16_t* partials, int splits, const float* w,
+                                     uint16_t* normalized, int rows, int hidden, float eps, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+#define NEMO_NORM16(S) \
+  rmsnorm_kernel<S, true><<<rows, 256, 0, stream>>>(x, partials, splits, rows, w, normalized, hidden, eps)
+  switch (splits) {
+    case 2: NEMO_NORM16(2); break;
+    case 3: NEMO_NORM16(3); break;
+    case 4: NEMO_NORM16(4); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef NEMO_NORM16
   return hipGetLastError();
 }
 

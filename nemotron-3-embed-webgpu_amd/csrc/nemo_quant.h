@@ -41,6 +41,8 @@ enum GemmEpilogue : int {
   kEpiStore = 0,    // out f16 [m, ldo]: f16(sum)
   kEpiPartial = 1,  // out float [splits][m][ldo]: the fp32 sum of each K split
   kEpiSwiGLU = 2,   // out f16 [m, ldo]: silu(g) * u over rows interleaved per 128-row tile
+  kEpiPartial16 = 3,  // out f16 [splits][m][ldo]: each K split's fp32 sum rounded to f16
+                      // (half kEpiPartial's bytes; the encoder's residual projections)
 };
 
 // Y[m, n] = f16( sum_k X[m, k] * W[n, k] ), fp32 accumulate. X is f16 with
