@@ -80,6 +80,13 @@ const char* nemo_last_error(void);
 /* Library version string. */
 const char* nemo_version(void);
 
+/* Testing hook, no counterpart in the reference: the calling thread's
+ * `checks`-th HIP status check from now on (counting every HIP call the
+ * library makes and checks on that thread, launches included) fails as if
+ * that call had returned an error, so tests can end an enqueue partway with
+ * kernels already queued. 0 turns it off. */
+void nemo_debug_fail_after(int32_t checks);
+
 /* Open a context on HIP device `device` (replaces requestWebGPUDevice,
  * src/webgpu/device.ts:6-24). */
 nemo_status nemo_init(int32_t device, nemo_ctx** out);
@@ -135,7 +142,9 @@ nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, co
 /* Same graph with ids and out as device pointers, enqueued on `stream`
  * (hipStream_t; NULL = the plan's own stream); lengths are host values.
  * Returns once enqueued. Work of the plan enqueued earlier on another stream
- * is waited for on the device first (the runs share the plan's buffers). */
+ * is waited for on the device first (the runs share the plan's buffers). If
+ * the enqueue fails partway, the call drains `stream` before it returns the
+ * error, and later calls on the plan still order after what was queued. */
 nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const uint32_t* lengths, size_t n_lengths,
                                  float* d_out, void* stream);
 
@@ -211,7 +220,10 @@ nemo_status nemo_weight_matmul(nemo_weight* weight, const uint16_t* d_x, int32_t
  * would exceed that size fails with NEMO_ERR_INVALID before launching
  * anything. Every call on one GPU shares the array: calls that overlap on
  * one GPU (concurrent streams, or host threads) race and must be ordered by
- * the caller. */
+ * the caller. Under HIP graph capture: make one eager call of the same
+ * shape and algorithm first (the first call of a kernel sets its LDS size
+ * attribute); the captured launches record no memset, and replays equal
+ * eager calls bit for bit (tests/test_zz_no_alloc.py). */
 nemo_status nemo_weight_matmul_static(nemo_weight* weight, const uint16_t* d_x, int32_t m, uint16_t* d_y,
                                       int32_t algo, void* stream);
 
@@ -225,6 +237,16 @@ nemo_status nemo_weight_dequantize(nemo_weight* weight, float* d_out, void* stre
  * n_values must be a whole number of blocks. */
 nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_values, float* d_out_f32,
                             uint16_t* d_out_f16, void* stream);
+
+/* Roofline probe, no counterpart in the reference: the floors the HBM-bound
+ * kernels are measured against. bytes == 0 launches one empty kernel (the
+ * cost of a launch); otherwise one kernel reads `bytes` (a multiple of 16)
+ * at the 16-byte aligned device pointer d_src once, with fully coalesced
+ * 16-byte loads, `loads_per_thread` (1, 2, 4 or 8) per thread, and does
+ * nothing else: the least time a kernel reading those bytes in one launch
+ * takes. d_sink is a device buffer of 256 uint32 the kernel may write. */
+nemo_status nemo_probe_stream(const void* d_src, size_t bytes, int32_t loads_per_thread, uint32_t* d_sink,
+                              void* stream);
 
 /* ---- offline requantization (src/gguf/quantization.ts:77-131) ------------ */
 

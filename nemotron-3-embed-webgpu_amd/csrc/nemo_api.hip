@@ -33,7 +33,13 @@ struct NemoError : std::runtime_error {
 
 [[noreturn]] void fail(nemo_status s, const std::string& m) { throw NemoError(s, m); }
 
+// Testing hook (nemo_debug_fail_after): the calling thread's n-th HIP status
+// check from now fails as if that call had returned an error.
+thread_local int g_fail_after = 0;
+
 void hip_check(hipError_t e, const char* what) {
+  if (g_fail_after > 0 && --g_fail_after == 0 && e == hipSuccess)
+    fail(NEMO_ERR_DEVICE, std::string(what) + ": injected failure");
   if (e == hipSuccess) return;
   if (e == hipErrorOutOfMemory) fail(NEMO_ERR_OOM, std::string(what) + ": out of device memory");
   fail(NEMO_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
@@ -340,10 +346,32 @@ struct nemo_plan {
 static void plan_begin(nemo_plan* p, hipStream_t s) {
   if (p->last_stream && p->last_stream != s) hip_check(hipStreamWaitEvent(s, p->done, 0), "hipStreamWaitEvent");
 }
-static void plan_end(nemo_plan* p, hipStream_t s) {
-  hip_check(hipEventRecord(p->done, s), "hipEventRecord");
-  p->last_stream = s;
-}
+// The end mark is recorded however the enqueue ends: a launch that fails
+// partway leaves the kernels before it queued on `s`, and later runs on other
+// streams, read_buffer and destroy must still wait for them. A failed enqueue
+// also drains `s` before the error returns (its queued copies may still read
+// the plan's pinned staging, which the next call overwrites), and so does a
+// failed record.
+struct PlanEnqueue {
+  nemo_plan* p;
+  hipStream_t s;
+  int unwinding;
+  PlanEnqueue(nemo_plan* plan, hipStream_t stream)
+      : p(plan), s(stream), unwinding(std::uncaught_exceptions()) {
+    plan_begin(p, s);
+  }
+  ~PlanEnqueue() {
+    const bool failed = std::uncaught_exceptions() > unwinding;
+    const bool recorded = hipEventRecord(p->done, s) == hipSuccess;
+    if (recorded) p->last_stream = s;
+    if (failed || !recorded) {
+      (void)hipStreamSynchronize(s);
+      (void)hipGetLastError();
+    }
+  }
+  PlanEnqueue(const PlanEnqueue&) = delete;
+  PlanEnqueue& operator=(const PlanEnqueue&) = delete;
+};
 // Blocks until all of the plan's enqueued work, on any stream, is done.
 static void plan_wait(nemo_plan* p) {
   if (p->last_stream) hip_check(hipEventSynchronize(p->done), "hipEventSynchronize");
@@ -389,6 +417,8 @@ void nemo_dims_reference(nemo_dims* out) {
 const char* nemo_last_error(void) { return g_last_error.c_str(); }
 
 const char* nemo_version(void) { return "libnemo 0.1 gfx950"; }
+
+void nemo_debug_fail_after(int32_t checks) { g_fail_after = checks > 0 ? checks : 0; }
 
 nemo_status nemo_init(int32_t device, nemo_ctx** out) {
   return guarded([&] {
@@ -1135,13 +1165,14 @@ nemo_status nemo_plan_run(nemo_plan* plan, const uint32_t* ids, size_t n_ids, co
     check_ids_host(plan, ids, n_ids, src);
     const size_t H = plan->model->dims.hidden;
     hipStream_t s = plan->stream;
-    plan_begin(plan, s);
-    memcpy(plan->h_ids, ids, n_ids * 4);
-    hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
-    enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s, [](int, bool) {});
-    hip_check(hipMemcpyAsync(plan->h_out, plan->out.get(), (size_t)plan->batch * H * 4, hipMemcpyDeviceToHost, s),
-              "readback");
-    plan_end(plan, s);
+    {
+      PlanEnqueue enqueue(plan, s);
+      memcpy(plan->h_ids, ids, n_ids * 4);
+      hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
+      enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s, [](int, bool) {});
+      hip_check(hipMemcpyAsync(plan->h_out, plan->out.get(), (size_t)plan->batch * H * 4, hipMemcpyDeviceToHost, s),
+                "readback");
+    }
     hip_check(hipStreamSynchronize(s), "run");
     memcpy(out, plan->h_out, (size_t)plan->batch * H * 4);
   });
@@ -1156,9 +1187,8 @@ nemo_status nemo_plan_run_device(nemo_plan* plan, const uint32_t* d_ids, const u
     Ragged src, dst;
     ragged_tables(plan, lengths, n_lengths, src, dst);
     hipStream_t s = stream ? (hipStream_t)stream : plan->stream;
-    plan_begin(plan, s);
+    PlanEnqueue enqueue(plan, s);
     enqueue_graph(plan, d_ids, src, dst, d_out, s, [](int, bool) {});
-    plan_end(plan, s);
   });
 }
 
@@ -1172,27 +1202,35 @@ nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids
     ragged_tables(plan, lengths, n_lengths, src, dst);
     check_ids_host(plan, ids, n_ids, src);
     hipStream_t s = plan->stream;
-    plan_begin(plan, s);
-    memcpy(plan->h_ids, ids, n_ids * 4);
-    hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
     // One event pair per stage instance, like the reference's one timestamp
-    // pair per compute pass.
+    // pair per compute pass (destroyed however the call ends).
     const int instances = 3 + plan->model->dims.layers * 8;
-    std::vector<hipEvent_t> events(2 * instances);
+    std::vector<hipEvent_t> events(2 * instances, nullptr);
+    struct EventsFree {
+      std::vector<hipEvent_t>& v;
+      ~EventsFree() {
+        for (auto& e : v)
+          if (e) (void)hipEventDestroy(e);
+      }
+    } events_free{events};
     for (auto& e : events) hip_check(hipEventCreate(&e), "hipEventCreate");
     std::vector<int> names;
     int next = 0;
-    enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s,
-                  [&](int stage, bool begin) {
-                    if (begin) {
-                      names.push_back(stage);
-                      hip_check(hipEventRecord(events[2 * next], s), "hipEventRecord");
-                    } else {
-                      hip_check(hipEventRecord(events[2 * next + 1], s), "hipEventRecord");
-                      ++next;
-                    }
-                  });
-    plan_end(plan, s);
+    {
+      PlanEnqueue enqueue(plan, s);
+      memcpy(plan->h_ids, ids, n_ids * 4);
+      hip_check(hipMemcpyAsync(plan->ids.get(), plan->h_ids, n_ids * 4, hipMemcpyHostToDevice, s), "upload ids");
+      enqueue_graph(plan, (const uint32_t*)plan->ids.get(), src, dst, (float*)plan->out.get(), s,
+                    [&](int stage, bool begin) {
+                      if (begin) {
+                        names.push_back(stage);
+                        hip_check(hipEventRecord(events[2 * next], s), "hipEventRecord");
+                      } else {
+                        hip_check(hipEventRecord(events[2 * next + 1], s), "hipEventRecord");
+                        ++next;
+                      }
+                    });
+    }
     hip_check(hipStreamSynchronize(s), "profile");
     for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
     for (int i = 0; i < next; ++i) {
@@ -1200,7 +1238,6 @@ nemo_status nemo_plan_profile(nemo_plan* plan, const uint32_t* ids, size_t n_ids
       hip_check(hipEventElapsedTime(&ms, events[2 * i], events[2 * i + 1]), "hipEventElapsedTime");
       stage_ms[names[i]] += ms;
     }
-    for (auto& e : events) (void)hipEventDestroy(e);
   });
 }
 
@@ -1356,6 +1393,22 @@ nemo_status nemo_dequantize(int32_t ggml_type, const void* d_raw, int64_t n_valu
   });
 }
 
+
+nemo_status nemo_probe_stream(const void* d_src, size_t bytes, int32_t loads_per_thread, uint32_t* d_sink,
+                              void* stream) {
+  return guarded([&] {
+    if (bytes == 0) {
+      hip_check(launch_probe_empty((hipStream_t)stream), "empty launch");
+      return;
+    }
+    if (!d_src || !d_sink) fail(NEMO_ERR_INVALID, "null argument");
+    if (bytes % 16 || ((uintptr_t)d_src & 15)) fail(NEMO_ERR_INVALID, "the probe reads whole 16-byte vectors");
+    if (loads_per_thread != 1 && loads_per_thread != 2 && loads_per_thread != 4 && loads_per_thread != 8)
+      fail(NEMO_ERR_INVALID, "loads_per_thread must be 1, 2, 4 or 8");
+    hip_check(launch_probe_stream(d_src, (int64_t)bytes, loads_per_thread, d_sink, (hipStream_t)stream),
+              "streaming probe");
+  });
+}
 
 nemo_status nemo_requantize_q40(nemo_ctx* ctx, int32_t src_type, const void* src, size_t n_src, int64_t k, int64_t n,
                                 void* out, size_t out_bytes) {

@@ -172,6 +172,12 @@ hipError_t launch_gemv_ex(const uint16_t* x, int ldx, const QWeight& w, int m, i
 hipError_t launch_dequant_raw(int type, const uint8_t* raw, int64_t n_blocks, float* out_f32,
                               uint16_t* out_f16, hipStream_t stream);
 
+// Roofline probes (nemo_probe.hip): one empty launch; one read of `bytes`
+// (a multiple of 16, 16-byte aligned) with `loads` (1, 2, 4 or 8) 16-byte
+// loads per thread. `sink` holds 256 words and is never written in practice.
+hipError_t launch_probe_empty(hipStream_t stream);
+hipError_t launch_probe_stream(const void* src, int64_t bytes, int loads, uint32_t* sink, hipStream_t stream);
+
 // requantizeMatrixToQ40 on the device: raw GGUF Q4_K / Q6_K / Q4_0 rows of a
 // k x n matrix (k % 256 == 0) -> n * k / 32 GGUF Q4_0 blocks (18 bytes),
 // bit-exact with the reference's JavaScript (nemo_requant.hip).

@@ -21,14 +21,14 @@ STATIC_SCRATCH_BYTES = 64 << 20  # NEMO_STATIC_SCRATCH_BYTES
 
 # Every symbol include/nemo.h declares.
 EXPORTED = [
-    "nemo_dims_reference", "nemo_last_error", "nemo_version", "nemo_init", "nemo_shutdown",
+    "nemo_dims_reference", "nemo_last_error", "nemo_version", "nemo_debug_fail_after", "nemo_init", "nemo_shutdown",
     "nemo_model_create", "nemo_model_set_tensor", "nemo_model_synthesize", "nemo_model_finalize",
     "nemo_model_get_tensor", "nemo_model_destroy", "nemo_plan_create", "nemo_plan_run", "nemo_plan_run_device",
     "nemo_plan_profile", "nemo_profile_stage_count", "nemo_profile_stage_name", "nemo_plan_destroy",
     "nemo_plan_shape", "nemo_plan_read_buffer",
     "nemo_weight_create", "nemo_weight_destroy", "nemo_weight_matmul", "nemo_weight_matmul_static",
     "nemo_weight_dequantize", "nemo_dequantize",
-    "nemo_requantize_q40",
+    "nemo_requantize_q40", "nemo_probe_stream",
 ]
 
 
@@ -71,6 +71,7 @@ def load() -> ctypes.CDLL:
         "nemo_dims_reference": (None, [ctypes.POINTER(Dims)]),
         "nemo_last_error": (ctypes.c_char_p, []),
         "nemo_version": (ctypes.c_char_p, []),
+        "nemo_debug_fail_after": (None, [i32]),
         "nemo_init": (i32, [i32, pp]),
         "nemo_shutdown": (i32, [vp]),
         "nemo_model_create": (i32, [vp, ctypes.POINTER(Dims), pp]),
@@ -95,6 +96,7 @@ def load() -> ctypes.CDLL:
         "nemo_weight_dequantize": (i32, [vp, vp, vp]),
         "nemo_dequantize": (i32, [i32, vp, ctypes.c_int64, vp, vp, vp]),
         "nemo_requantize_q40": (i32, [vp, i32, vp, sz, ctypes.c_int64, ctypes.c_int64, vp, sz]),
+        "nemo_probe_stream": (i32, [vp, sz, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

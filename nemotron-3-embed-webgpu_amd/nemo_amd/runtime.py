@@ -15,7 +15,7 @@ import asyncio
 import ctypes
 import math
 import threading
-from typing import Iterable
+from typing import Awaitable, Iterable
 
 import numpy as np
 
@@ -141,19 +141,36 @@ class NemotronHipPlan:
         self._enter()
         return self._run_entered(ids, lengths)
 
-    def run(self, ids, lengths) -> "asyncio.Future[list[np.ndarray]]":
+    def run(self, ids, lengths) -> "Awaitable[list[np.ndarray]]":
         """EmbeddingPlan.run (src/webgpu/embedding-engine.ts:8): awaitable.
-        The run is counted in flight as this call returns (as the
-        reference's run has written its buffers and submitted by then), and
-        executes on a worker thread so that distinct plans overlap."""
+
+        Called inside a running event loop it returns a future: the run is
+        counted in flight as this call returns (as the reference's run has
+        written its buffers and submitted by then) and executes on a worker
+        thread of that loop, so that distinct plans overlap. Called with no
+        loop running (``asyncio.run(plan.run(ids, lengths))``) it returns a
+        coroutine that enters the run when it is first awaited, on the loop
+        that awaits it; a coroutine never awaited leaves no run counted."""
         ids, lengths = _u32(ids).reshape(-1).copy(), _u32(lengths).reshape(-1).copy()
-        self._enter()
         try:
             loop = asyncio.get_running_loop()
+        except RuntimeError:
+            return self._run_later(ids, lengths)
+        self._enter()
+        try:
             return loop.run_in_executor(None, self._run_entered, ids, lengths)
         except BaseException:
             self._leave()
             raise
+
+    async def _run_later(self, ids: np.ndarray, lengths: np.ndarray) -> list[np.ndarray]:
+        self._enter()
+        try:
+            fut = asyncio.get_running_loop().run_in_executor(None, self._run_entered, ids, lengths)
+        except BaseException:
+            self._leave()
+            raise
+        return await fut
 
     def run_device(self, d_ids: int, lengths, d_out: int, stream: int = 0) -> None:
         """Enqueue on `stream` with ids and output already in device memory."""
@@ -354,6 +371,14 @@ def dequantize_device(ggml_type: int, d_raw: int, n_values: int, d_out_f32: int 
     """Decode raw GGUF blocks already in device memory."""
     check(_lib.load().nemo_dequantize(ggml_type, ctypes.c_void_p(d_raw), n_values, ctypes.c_void_p(d_out_f32 or None),
                                       ctypes.c_void_p(d_out_f16 or None), ctypes.c_void_p(stream or None)))
+
+
+def probe_stream(d_src: int, nbytes: int, loads_per_thread: int, d_sink: int, stream: int = 0) -> None:
+    """Roofline probe: one kernel reading `nbytes` at d_src once with
+    coalesced 16-byte loads (nbytes == 0: one empty launch); d_sink holds 256
+    uint32 (include/nemo.h nemo_probe_stream)."""
+    check(_lib.load().nemo_probe_stream(ctypes.c_void_p(d_src or None), nbytes, loads_per_thread,
+                                        ctypes.c_void_p(d_sink or None), ctypes.c_void_p(stream or None)))
 
 
 def requantize_q40(src_type: int, data, k: int, n: int, device: int = 0) -> bytes:

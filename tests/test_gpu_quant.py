@@ -339,3 +339,22 @@ def test_q40_matmul_all_paths(torch_cuda, m, n, k):
     w32 = oracle.dequantize(2, raw).reshape(n, k)[cols]
     for algo, y in outs.items():
         _check_matmul(y.view(np.float16)[:, cols], x16, w32)
+
+
+def test_roofline_probes(torch_cuda):
+    """The streaming probe reads whole buffers (any loads per thread, a
+    partial last workgroup) and leaves its sink untouched; an empty launch
+    runs; misaligned or ragged sizes are refused before launching."""
+    torch = torch_cuda
+    src = torch.zeros((1 << 20,), dtype=torch.int32, device="cuda")  # xor 0 never equals the probe's magic
+    sink = torch.full((256,), 7, dtype=torch.int32, device="cuda")
+    for loads in (1, 2, 4, 8):
+        for nbytes in (16, 4096 * 4 + 16, src.numel() * 4):
+            rt.probe_stream(src.data_ptr(), nbytes, loads, sink.data_ptr())
+    rt.probe_stream(0, 0, 1, 0)
+    torch.cuda.synchronize()
+    assert bool((sink == 7).all())
+    with pytest.raises(rt.NemoError, match="16-byte"):
+        rt.probe_stream(src.data_ptr() + 4, 64, 1, sink.data_ptr())
+    with pytest.raises(rt.NemoError, match="loads_per_thread"):
+        rt.probe_stream(src.data_ptr(), 64, 3, sink.data_ptr())

@@ -109,3 +109,35 @@ def test_failed_run_settles_the_count(fake):
         assert fake.calls == ["create", "run", "destroy"] and plan.pending == 0
 
     asyncio.run(scenario())
+
+
+def test_run_awaited_from_asyncio_run(fake):
+    """asyncio.run(plan.run(ids, lengths)): with no loop running when run() is
+    called, it returns a coroutine that enters the run when awaited."""
+    plan = rt.NemotronHipPlan(MODEL, 1, 2)
+    fake.release.set()
+    coro = plan.run(np.arange(2), [2])
+    assert plan.pending == 0  # not entered until awaited
+    out = asyncio.run(coro)
+    assert len(out) == 1 and out[0].shape == (4,)
+    assert fake.calls == ["create", "run"] and plan.pending == 0
+    plan.destroy()
+    assert fake.calls == ["create", "run", "destroy"]
+
+
+def test_unawaited_coroutine_leaves_no_run_counted(fake):
+    plan = rt.NemotronHipPlan(MODEL, 1, 2)
+    coro = plan.run(np.arange(2), [2])
+    coro.close()
+    assert plan.pending == 0
+    plan.destroy()
+    assert fake.calls == ["create", "destroy"]
+
+
+def test_coroutine_awaited_after_destroy_fails(fake):
+    plan = rt.NemotronHipPlan(MODEL, 1, 2)
+    coro = plan.run(np.arange(2), [2])
+    plan.destroy()
+    with pytest.raises(rt.NemoError, match="plan was destroyed"):
+        asyncio.run(coro)
+    assert fake.calls == ["create", "destroy"]

@@ -93,3 +93,55 @@ def test_static_scratch_rejects_oversize(torch_cuda):
     got, want = _both(torch, w, x16, 120, _lib.MATMUL_GEMV)
     assert np.array_equal(got, want)
     w.destroy()
+
+
+GRAPH_CASES = [
+    # (type, n, k, algo, m): the scratch kinds, each captured into a HIP graph
+    (12, 16384, 2048, _lib.MATMUL_TWO_PASS, 600),   # f16 expansion, then the f16 MFMA GEMM
+    (12, 5120, 2048, _lib.MATMUL_GEMM_SPLIT, 64),   # 64-row tiles, fp32 partials, fixed-order reduction
+    (14, 2048, 8192, _lib.MATMUL_GEMV, 160),        # GEMV with K split 4 ways, fp32 partials
+]
+
+
+@pytest.mark.parametrize("type_,n,k,algo,m", GRAPH_CASES)
+def test_static_scratch_under_graph_capture(torch_cuda, type_, n, k, algo, m):
+    """nemo_weight_matmul_static captured into a HIP graph (torch.cuda.graph)
+    after one eager call of the same shape, which configures its kernels.
+    The paths record no memset (every kernel writes each scratch element it
+    reads). The graph is replayed three times with a new X written in place
+    before each replay and eager calls of the allocating entry point between
+    replays; every replay must equal the eager result for its X bit for bit."""
+    torch = torch_cuda
+    L = _lib.load()
+    seed = 9501 + n + k + type_ + algo
+    w = _weight(type_, n, k, seed)
+    xs = [synth.normal(seed + 1 + i, m * k).astype(np.float16).reshape(m, k) for i in range(4)]
+    dx = torch.from_numpy(xs[0].view(np.int16).copy()).cuda()
+    dy = torch.full((m, n), NAN16, dtype=torch.int16, device="cuda")
+    dref = torch.full((m, n), NAN16, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        _lib.check(L.nemo_weight_matmul_static(w._ptr, ctypes.c_void_p(dx.data_ptr()), m,
+                                               ctypes.c_void_p(dy.data_ptr()), algo,
+                                               ctypes.c_void_p(stream.cuda_stream)))
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        _lib.check(L.nemo_weight_matmul_static(w._ptr, ctypes.c_void_p(dx.data_ptr()), m,
+                                               ctypes.c_void_p(dy.data_ptr()), algo,
+                                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    for i in range(1, 4):
+        dx.copy_(torch.from_numpy(xs[i].view(np.int16).copy()))
+        dy.fill_(NAN16)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = dy.cpu().numpy()
+        _call(L.nemo_weight_matmul, w, dx, m, dref, algo)
+        torch.cuda.synchronize()
+        want = dref.cpu().numpy()
+        assert np.array_equal(got, want), f"replay {i}: {np.count_nonzero(got != want)} elements differ"
+        assert np.all(np.isfinite(got.view(np.float16)))
+    del g
+    w.destroy()
