@@ -788,8 +788,21 @@ static int tail_main_rows(int m, int n) {
 // after the merge); 256 x 128 tiles for unsplit problems with at least 64 of
 // them (the QKV projection). Split-K problems with fewer 256-column tiles do
 // better on the fused 128-row tiles, of which two or more fit on a CU.
-static int two_pass_tile(const QWeight& w, int m, int splits) {
+static int two_pass_tile(const QWeight& w, int m, int splits, bool with_side = false) {
   const int mt = (m + kBigBM - 1) / kBigBM;
+  // A launch that carries side work (another matrix's expansion) and whose
+  // 256 x 256 tiles fill 3/4 to all of a round: those tiles, so the idle CUs
+  // run the side work beside them from the start. Measured on the encoder's
+  // down projection after the merge (Q6_K 2048 x 8192, K split 4 ways, 1536
+  // tokens, the next layer's QKV and O expansion as side work): 192 tiles of
+  // 256 x 256 took the 16 x 150 pass 4.71 -> 4.60 ms against 512 tiles of
+  // 192 x 128 (two per CU, which start the side work only as they finish),
+  // although alone the 192 x 128 tiles are faster (61.2 against 67.7 us).
+  // The same launch on 160 tiles at 2400 tokens (K split 2) was not faster.
+  if (with_side && w.n % 256 == 0 && splits > 1) {
+    const int t256 = mt * (w.n / 256) * splits;
+    if (4 * t256 >= 3 * 256 && t256 <= 256) return kF16T256x256;
+  }
   if (w.n % 256 == 0 && mt * (w.n / 256) * splits >= (w.type == kQ6_K ? 192 : 256)) {
     // 192-row tiles (4 waves; measured at ~0.83 of the 256-row tiles' rate
     // per flop) when their rounds of 256 workgroups cost less: 1536 tokens
@@ -861,6 +874,9 @@ static int two_pass_tile(const QWeight& w, int m, int splits) {
   return kF16None;
 }
 
+// Whether the problem takes the two-pass path. Side work never decides
+// that: its rule in two_pass_tile only picks among two-pass tilings of
+// split problems, which take the two-pass path without it too.
 bool gemm_two_pass(const QWeight& w, int m, int splits) {
   return !use_mid(w, m, splits) && two_pass_tile(w, m, splits) != kF16None;
 }
@@ -1004,7 +1020,8 @@ static hipError_t launch_fused(const uint16_t* x, int ldx, const QWeight& w, int
   if (w.type != kQ4_K && w.type != kQ6_K && w.type != kQ4_0) return hipErrorInvalidValue;
   const int kchunk = w.k / splits;
   if (forced < 0 && use_mid(w, m, splits)) forced = kVarMid;
-  const int tile = (wexp && forced < 0) ? two_pass_tile(w, m, splits) : kF16None;
+  const int tile = (wexp && forced < 0) ? two_pass_tile(w, m, splits, side && side->count && side->nblocks > 0)
+                                         : kF16None;
   if (tile != kF16None)
     return launch_two_pass(x, ldx, w, m, epilogue, splits, out, ldo, wexp, stream, tile, expanded, side);
   const int var = forced >= 0 ? forced : gemm_variant(w, m, splits);
