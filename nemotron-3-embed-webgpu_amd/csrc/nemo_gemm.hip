@@ -21,6 +21,7 @@
 // token's result does not depend on how many other tokens share the batch.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -98,6 +99,53 @@ __device__ __forceinline__ void gemm_epilogue(const float16v (&acc)[MI][4], int 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = rbase + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row >= M) continue;
+          if constexpr (EPI == kEpiStore)
+            ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
+          else if constexpr (EPI == kEpiPartial16)
+            ((uint16_t*)out)[((size_t)split * M + row) * ldo + col] = f2h(acc[i][j][r]);
+          else
+            ((float*)out)[((size_t)split * M + row) * ldo + col] = acc[i][j][r];
+        }
+      }
+  }
+}
+
+// The same epilogue for a wave owning MI16 x 8 blocks of 16 x 16 starting at
+// (rbase0, cbase): lane l, register r of block (i, j) is row rbase0 + 16i +
+// 4(l/16) + r, column cbase + 16j + l%16. For kEpiSwiGLU blocks j < 4 are the
+// gate features cbase/2 + 16j + l%16 and blocks j + 4 their up rows.
+template <int EPI, int MI16>
+__device__ __forceinline__ void gemm_epilogue16(const float4v (&acc)[MI16][8], int rbase0, int cbase, int lane, int M,
+                                                int N, void* out, int ldo, int split) {
+  const int rbase = rbase0 + 4 * (lane >> 4);
+  if constexpr (EPI == kEpiSwiGLU) {
+    uint16_t* y = (uint16_t*)out;
+#pragma unroll
+    for (int i = 0; i < MI16; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = (cbase >> 1) + j * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rbase + i * 16 + r;
+          if (row < M) {
+            const float g = (float)(half_t)acc[i][j][r];
+            const float u = (float)(half_t)acc[i][j + 4][r];
+            y[(size_t)row * ldo + col] = f2h(g / (1.0f + expf(-g)) * u);
+          }
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MI16; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int col = cbase + j * 16 + (lane & 15);
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rbase + i * 16 + r;
           if (row >= M) continue;
           if constexpr (EPI == kEpiStore)
             ((uint16_t*)out)[(size_t)row * ldo + col] = f2h(acc[i][j][r]);
@@ -548,7 +596,17 @@ __host__ __device__ inline void f16_tile_coords(int i, int ntx, int nty, int nti
 // f16_tile_coords gives it; the workgroups past the tiles do `side`, another
 // matrix's expansion, on the CUs the tiles leave idle (dispatched after the
 // tiles, so they never delay one).
-template <int EPI, int BN, int WM, int MI>
+//
+// K16: 16 x 16 x 32 MFMAs (each wave's MI 32-row blocks as 2 MI 16-row
+// blocks, 8 column blocks of 16) instead of 32 x 32 x 16. Every output sums
+// the same f16 products in the same k order, and the two forms give
+// bit-identical results (the fused kernels use 32 x 32 x 16). In the 16 x
+// 150 encoder pass the 16 x 16 form runs the 4- and 8-wave tiles whose waves
+// hold 64 or 96 rows 4-9 % faster (gate/up 256 x 256 137.0 -> 124.5 us, 384 x
+// 256 103.4 -> 99.2, down 256 x 256 61.6 -> 57.5); with 32-row waves
+// (128 x 256) and on the 2-wave 192 x 128 tile it gains nothing or loses up
+// to 1.3 %, and they keep 32 x 32.
+template <int EPI, int BN, int WM, int MI, bool K16>
 __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint16_t* __restrict__ x, int ldx,
                                                                      const uint16_t* __restrict__ wt, int N, int K,
                                                                      int M, int kchunk, void* __restrict__ out,
@@ -579,59 +637,106 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
 
   // Each copy instruction moves 8 whole rows: lane l -> row R + l/8, slot
   // l%8 holding logical chunk (l%8) ^ f(row). Wave w copies X rows
-  // [8 XI w, +8 XI) and W rows [8 WI w, +8 WI).
-  const uint16_t* xsrc[XI];
-  const uint16_t* wsrc[WI];
+  // [8 XI w, +8 XI) and W rows [8 WI w, +8 WI). Addresses are the tile's
+  // first row (uniform) plus 32-bit element offsets (at most BM ldx and
+  // BN K), half the registers of per-lane pointers.
+  const uint16_t* xtile = x + (size_t)m0 * ldx;
+  const uint16_t* wtile = wt + (size_t)n0 * K;
+  int xoff[XI], woff[WI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int r = 8 * XI * wave + 8 * i + (lane >> 3);
-    xsrc[i] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * ((lane & 7) ^ xswz(r));
+    xoff[i] = (min(m0 + r, M - 1) - m0) * ldx + 8 * ((lane & 7) ^ xswz(r));
   }
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     const int r = 8 * WI * wave + 8 * i + (lane >> 3);
-    wsrc[i] = wt + (size_t)min(n0 + r, N - 1) * K + 8 * ((lane & 7) ^ xswz(r));
+    woff[i] = (min(n0 + r, N - 1) - n0) * K + 8 * ((lane & 7) ^ xswz(r));
   }
   auto copy = [&](int stage, int k0) {
+    const uint16_t* xk = xtile + k0;
+    const uint16_t* wk = wtile + k0;
 #pragma unroll
     for (int i = 0; i < XI; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(xk + xoff[i]),
                                        (lds_void*)(sX + stage * XSTAGE + (8 * XI * wave + 8 * i) * 128), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < WI; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(wsrc[i] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(wk + woff[i]),
                                        (lds_void*)(sW + stage * WSTAGE + (8 * WI * wave + 8 * i) * 128), 16, 0, 0);
   };
 
-  float16v acc[MI][4];
+  // Accumulators: MI x 4 blocks of 32 x 32, or 2 MI x 8 blocks of 16 x 16.
+  constexpr int AI = K16 ? 2 * MI : MI, AJ = K16 ? 8 : 4;
+  using Acc = std::conditional_t<K16, float4v, float16v>;
+  Acc acc[AI][AJ];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < AI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < AJ; ++j) acc[i][j] = Acc{};
 
   auto mfma_step = [&](int stage) {
     const uint8_t* xs = sX + stage * XSTAGE;
     const uint8_t* ws = sW + stage * WSTAGE;
+    if constexpr (K16) {
+      // Two k steps of 32: lane l holds k 8(l/16) .. +7 of row or column l%16.
+      // Beside the 192 accumulator registers of the 384 x 256 tile's waves
+      // only half the A fragments and 2 B fragments fit at a time (its B
+      // fragments are read twice; any more live fragments spill).
+      constexpr int IH = (WM == 4 && MI == 3) ? 2 : 1;  // A fragments in IH parts
+      constexpr int JG = (WM == 4 && MI == 3) ? 2 : 4;  // B fragments at a time
+      constexpr int AP = AI / IH;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int c = 2 * ks + (lane >> 5);
-      half8v af[MI], bf[4];
+      for (int ks = 0; ks < 2; ++ks) {
+        const int c = 4 * ks + (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int r = wm * 32 * MI + i * 32 + (lane & 31);
-        af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
+        for (int ih = 0; ih < IH; ++ih) {
+          half8v af[AP];
+#pragma unroll
+          for (int i = 0; i < AP; ++i) {
+            const int r = wm * 32 * MI + (AP * ih + i) * 16 + (lane & 15);
+            af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
+          }
+#pragma unroll
+          for (int jg = 0; jg < 8 / JG; ++jg) {
+            half8v bf[JG];
+#pragma unroll
+            for (int j = 0; j < JG; ++j) {
+              const int r = wn * 128 + (JG * jg + j) * 16 + (lane & 15);
+              bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
+            }
+#pragma unroll
+            for (int i = 0; i < AP; ++i)
+#pragma unroll
+              for (int j = 0; j < JG; ++j)
+                acc[AP * ih + i][JG * jg + j] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[AP * ih + i][JG * jg + j], 0, 0, 0);
+            if constexpr (IH == 2) __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       }
+    } else {
+      // Four k steps of 16: lane l holds k 8(l/32) .. +7 of row or column l%32.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = wn * 128 + j * 32 + (lane & 31);
-        bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
+      for (int ks = 0; ks < 4; ++ks) {
+        const int c = 2 * ks + (lane >> 5);
+        half8v af[MI], bf[4];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int r = wm * 32 * MI + i * 32 + (lane & 31);
+          af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = wn * 128 + j * 32 + (lane & 31);
+          bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -654,7 +759,10 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
     copy(1, kat(s + 3));
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo, bz);
+  if constexpr (K16)
+    gemm_epilogue16<EPI, AI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo, bz);
+  else
+    gemm_epilogue<EPI, MI>(acc, m0 + wm * 32 * MI, n0 + wn * 128, lane, M, N, out, ldo, bz);
 }
 
 int gemm_splits(const QWeight& w, int m) {
@@ -959,10 +1067,11 @@ static void launch_f16(int epilogue, dim3 grid, const uint16_t* x, int ldx, cons
     kernel<<<ntiles + nside, threads, lds, stream>>>(x, ldx, wexp, w.n, w.k, m, kchunk, out, ldo, (int)grid.x,
                                                       (int)grid.y, ntiles, gw, e);
   };
-  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI>);
-  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI>);
-  else if (epilogue == kEpiPartial16) launch(gemm_f16_kernel<kEpiPartial16, BN, WM, MI>);
-  else launch(gemm_f16_kernel<kEpiSwiGLU, BN, WM, MI>);
+  constexpr bool k16 = WM == 4 && MI >= 2;  // 16 x 16 x 32 MFMAs on the 4- and 8-wave tiles of 64+ rows a wave
+  if (epilogue == kEpiStore) launch(gemm_f16_kernel<kEpiStore, BN, WM, MI, k16>);
+  else if (epilogue == kEpiPartial) launch(gemm_f16_kernel<kEpiPartial, BN, WM, MI, k16>);
+  else if (epilogue == kEpiPartial16) launch(gemm_f16_kernel<kEpiPartial16, BN, WM, MI, k16>);
+  else launch(gemm_f16_kernel<kEpiSwiGLU, BN, WM, MI, k16>);
 }
 
 static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, int m, int epilogue, int splits,

@@ -218,6 +218,34 @@ def test_two_pass_bit_identical_to_fused(torch_cuda, type_, m, n, k):
     _check_matmul(y[:, cols], x16, w_sample)
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (600, 2048, 2048),    # 256 x 256 tiles: 16 x 16 x 32 MFMAs, waves of 64 rows
+    (2400, 16384, 2048),  # 256 x 256 rows, the last 352 on 128 x 256 (32 x 32 x 16)
+    (1536, 2048, 6144),   # 384 x 256 or 192 x 256 tiles
+])
+def test_mfma_forms_bit_identical_wide_range(torch_cuda, m, n, k):
+    """The f16 GEMM's 16 x 16 x 32 MFMAs and the fused kernels' 32 x 32 x 16
+    round the same f32 sums at the same points: bit-identical results on
+    activations spread over 2^-10 .. 2^6 with random signs (sums that cancel
+    and long carries, where any other rounding order shows)."""
+    torch = torch_cuda
+    seed = 9107 + m + n + k
+    raw = synth.random_q4k(seed, n * k // 256)
+    e = synth.randint(seed + 1, m * k, -10, 6).astype(np.float64)
+    sign = np.where(synth.randint(seed + 2, m * k, 0, 2) == 0, -1.0, 1.0)
+    x16 = (sign * np.exp2(e) * (1.0 + synth.uniform(seed + 3, m * k))).astype(np.float16).reshape(m, k)
+    w = rt.QuantWeight(12, n, k, raw.tobytes())
+    dx = torch.from_numpy(x16.view(np.int16).copy()).cuda()
+    fused = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    two = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    w.matmul(dx.data_ptr(), m, fused.data_ptr(), _lib.MATMUL_GEMM)
+    w.matmul(dx.data_ptr(), m, two.data_ptr(), _lib.MATMUL_TWO_PASS)
+    torch.cuda.synchronize()
+    y = two.cpu().numpy().view(np.float16)
+    assert np.isfinite(y).all()
+    assert torch.equal(fused, two)
+
+
 @pytest.mark.parametrize("type_,m,n,k", [
     (12, 17, 5120, 2048),      # QKV of one 17-token request
     (12, 150, 12288, 2048),    # gate/up of one 150-token request
