@@ -681,38 +681,32 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
     if constexpr (K16) {
       // Two k steps of 32: lane l holds k 8(l/16) .. +7 of row or column l%16.
       // Beside the 192 accumulator registers of the 384 x 256 tile's waves
-      // only half the A fragments and 2 B fragments fit at a time (its B
-      // fragments are read twice; any more live fragments spill).
-      constexpr int IH = (WM == 4 && MI == 3) ? 2 : 1;  // A fragments in IH parts
+      // the B fragments go 2 at a time, each group's reads and MFMAs kept
+      // together (without the scheduling barrier, or with all 8 B fragments
+      // live, the compiler spills; reading A in two halves instead fits too
+      // but reads B twice, 6.5 % slower).
       constexpr int JG = (WM == 4 && MI == 3) ? 2 : 4;  // B fragments at a time
-      constexpr int AP = AI / IH;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int c = 4 * ks + (lane >> 4);
+        // Rows 16 i + l%16 share the swizzle of row l%16: one lane offset per
+        // operand and k step, the blocks at constant offsets of 2 KB.
+        const int c = 4 * ks + (lane >> 4), sw = 16 * (c ^ xswz(lane & 15));
+        const uint8_t* xa = xs + (wm * 32 * MI + (lane & 15)) * 128 + sw;
+        const uint8_t* wb = ws + (wn * 128 + (lane & 15)) * 128 + sw;
+        half8v af[AI];
 #pragma unroll
-        for (int ih = 0; ih < IH; ++ih) {
-          half8v af[AP];
+        for (int i = 0; i < AI; ++i) af[i] = *(const half8v*)(xa + i * 2048);
 #pragma unroll
-          for (int i = 0; i < AP; ++i) {
-            const int r = wm * 32 * MI + (AP * ih + i) * 16 + (lane & 15);
-            af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
-          }
+        for (int jg = 0; jg < 8 / JG; ++jg) {
+          half8v bf[JG];
 #pragma unroll
-          for (int jg = 0; jg < 8 / JG; ++jg) {
-            half8v bf[JG];
+          for (int j = 0; j < JG; ++j) bf[j] = *(const half8v*)(wb + (JG * jg + j) * 2048);
 #pragma unroll
-            for (int j = 0; j < JG; ++j) {
-              const int r = wn * 128 + (JG * jg + j) * 16 + (lane & 15);
-              bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
-            }
+          for (int i = 0; i < AI; ++i)
 #pragma unroll
-            for (int i = 0; i < AP; ++i)
-#pragma unroll
-              for (int j = 0; j < JG; ++j)
-                acc[AP * ih + i][JG * jg + j] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[AP * ih + i][JG * jg + j], 0, 0, 0);
-            if constexpr (IH == 2) __builtin_amdgcn_sched_barrier(0);
-          }
+            for (int j = 0; j < JG; ++j)
+              acc[i][JG * jg + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][JG * jg + j], 0, 0, 0);
+          if constexpr (JG == 2) __builtin_amdgcn_sched_barrier(0);
         }
       }
     } else {
