@@ -710,21 +710,18 @@ __global__ __launch_bounds__(WM * BN / 128 * 64) void gemm_f16_kernel(const uint
         }
       }
     } else {
-      // Four k steps of 16: lane l holds k 8(l/32) .. +7 of row or column l%32.
+      // Four k steps of 16: lane l holds k 8(l/32) .. +7 of row or column l%32
+      // (row blocks at constant offsets of 4 KB from one lane offset).
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const int c = 2 * ks + (lane >> 5);
+        const int c = 2 * ks + (lane >> 5), sw = 16 * (c ^ xswz(lane & 31));
+        const uint8_t* xa = xs + (wm * 32 * MI + (lane & 31)) * 128 + sw;
+        const uint8_t* wb = ws + (wn * 128 + (lane & 31)) * 128 + sw;
         half8v af[MI], bf[4];
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          const int r = wm * 32 * MI + i * 32 + (lane & 31);
-          af[i] = *(const half8v*)(xs + r * 128 + 16 * (c ^ xswz(r)));
-        }
+        for (int i = 0; i < MI; ++i) af[i] = *(const half8v*)(xa + i * 4096);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = wn * 128 + j * 32 + (lane & 31);
-          bf[j] = *(const half8v*)(ws + r * 128 + 16 * (c ^ xswz(r)));
-        }
+        for (int j = 0; j < 4; ++j) bf[j] = *(const half8v*)(wb + j * 4096);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
