@@ -1070,6 +1070,8 @@ static hipError_t launch_two_pass(const uint16_t* x, int ldx, const QWeight& w, 
                                   bool expanded = false, const SideExpand* side = nullptr) {
   const int bm = f16_bm(tile), bn = f16_bn(tile);
   if (epilogue == kEpiSwiGLU && w.n % bn) return hipErrorInvalidValue;
+  // gemm_f16_kernel addresses a tile's rows by 32-bit element offsets
+  if ((int64_t)bm * ldx > INT32_MAX || (int64_t)bn * w.k > INT32_MAX) return hipErrorInvalidValue;
   const int64_t threads = (int64_t)w.n * (w.k / 32);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (expanded) {
